@@ -1,0 +1,349 @@
+"""Benchmark of the paged GQA decode hot path on one MI355X.
+
+Headline (BASELINE.json metric): one decode *call* = KV append of the new token
++ split-KV GQA decode (load + merge) for one layer, at B=32, kv_len=4096 prior
+(4097 attended), H_q=14, H_kv=2, D=64, page_size 16, fp16.  The layer rotates
+over R distinct per-layer pools (R * pool bytes >= 512 MiB) so the 256 MB
+Infinity Cache cannot serve repeat reads.  Calls are captured in a hipGraph
+(R calls per graph, as a decode step walks the layers) and replayed.
+
+Prints ONE JSON line.  ``value`` = algorithmic GB/s of a call (higher is
+better); ``us_per_call`` is the same measurement as a time.  ``roofline`` rates
+the dominant kernel(s) (the decode op, timed alone with HIP events on the
+stream it runs on) against 8 TB/s.  ``cpu_baseline`` times the CPU oracle
+(the reference's semantics: torch gather + SDPA in fp32, numpy append) on
+this host on a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--config 2|3|4] [--no-cpu-baseline]
+    python bench.py --copy-calib      # plain copy kernel for rocprofv3 counter scaling
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "paged GQA decode µs/call + HBM GB/s (% of peak) at B=32 kv_len=4096"
+HBM_PEAK_GBPS = 8000.0
+MIN_ROTATION_BYTES = 512 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=800, help="decode calls timed (rounded up to a multiple of R)")
+    ap.add_argument("--warmup", type=int, default=80)
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
+    ap.add_argument("--splits", type=int, default=None, help="KV splits (default: the library's policy)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of graph replay")
+    ap.add_argument("--copy-calib", action="store_true")
+    ap.add_argument("--repeats", type=int, default=5)
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Layer:
+    """One layer's pools + the step inputs of a decode call."""
+
+    def __init__(self, kp, vp, q, k_new, v_new):
+        self.kp, self.vp, self.q, self.k_new, self.v_new = kp, vp, q, k_new, v_new
+
+
+def build_layers(case, dev, R: int, seed: int = 1):
+    """Layer 0 = the seeded oracle case; layers 1..R-1 = distinct random pools of the same shape."""
+    layers = [Layer(case.k_pool.to(dev), case.v_pool.to(dev), case.q.to(dev), case.k_new.to(dev),
+                    case.v_new.to(dev))]
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def rnd(t):
+        return (torch.randn(t.shape, generator=g, device=dev) * 0.5).half()
+
+    for _ in range(1, R):
+        layers.append(Layer(rnd(case.k_pool), rnd(case.v_pool), rnd(case.q), rnd(case.k_new),
+                            rnd(case.v_new)))
+    return layers
+
+
+def time_calls(fn_list, steps: int, warmup: int, use_graph: bool, repeats: int) -> tuple[float, int]:
+    """Median over repeats of the per-call time (us) of running fn_list round-robin."""
+    R = len(fn_list)
+    reps = max(1, -(-steps // R))
+    steps = reps * R
+    stream = torch.cuda.current_stream()
+
+    def run_all():
+        for f in fn_list:
+            f()
+
+    if use_graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            run_all()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run_all()
+        body = graph.replay
+    else:
+        body = run_all
+    for _ in range(max(1, -(-warmup // R))):
+        body()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(reps):
+            body()
+        end.record(stream)
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) * 1e3 / steps)
+    return statistics.median(times), steps
+
+
+def cpu_baseline(case, budget_s: float = 20.0, max_runs: int = 7):
+    """The oracle (reference semantics) on this host's cores: numpy append + torch gather/SDPA fp32."""
+    from oracle import paged_attention as ref
+
+    n_cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n_cores)
+
+    def one():
+        kp, vp = case.k_pool.clone(), case.v_pool.clone()
+        t0 = time.perf_counter()
+        ref.append_decode(kp, vp, case.k_new, case.v_new, case.slot_ids, case.lens_pool, case.block_table)
+        out = ref.decode_attention(case.q, kp, vp, case.attended, case.slot_ids, case.block_table)
+        return time.perf_counter() - t0, out
+
+    runs, spent = [], 0.0
+    for i in range(2 + max_runs):
+        dt, out = one()
+        spent += dt
+        if i >= 2:
+            runs.append(dt)
+        if len(runs) >= 5 and spent > budget_s:
+            break
+    return statistics.median(runs) * 1e6, len(runs), torch.get_num_threads(), out
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def copy_calibration(args):
+    """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE."""
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_()
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build's hot path is "
+              "single-GPU and launches no collectives.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    if args.copy_calib:
+        return copy_calibration(args)
+
+    import custom_inference_engine_amd as cie
+    from custom_inference_engine_amd import _native
+    from oracle import inputs, paged_attention as ref
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.config == 3:
+        return bench_mixed(args, cie, inputs, ref, dev)
+    case = inputs.config2(seed=0) if args.config == 2 else inputs.config4(seed=0)
+    splits = args.splits or (case.meta.get("n_splits") if args.config == 4 else None)
+    log(f"config {args.config}: B={case.B} attend={int(case.attended[0])} pool pages={case.k_pool.shape[0]}")
+
+    pool_bytes = 2 * case.k_pool.numel() * 2
+    R = max(1, -(-MIN_ROTATION_BYTES // pool_bytes))
+    layers = build_layers(case, dev, R)
+    c = case.to(dev)
+    slot_ids, lens_pool, bt = c.slot_ids, c.lens_pool, c.block_table
+    attended = (lens_pool[slot_ids] + 1).contiguous()
+    log(f"rotation: {R} layer pools x {pool_bytes / 2**20:.1f} MiB = {R * pool_bytes / 2**20:.0f} MiB")
+
+    outs = [None] * R
+
+    def call(i):
+        L = layers[i]
+
+        def f():
+            cie.kv_append_decode(L.kp, L.vp, L.k_new, L.v_new, slot_ids, lens_pool, bt)
+            outs[i] = cie.decode_gqa_attention(L.q, L.kp, L.vp, attended, slot_ids, bt, num_programs=splits)
+        return f
+
+    def decode_only(i):
+        L = layers[i]
+
+        def f():
+            outs[i] = cie.decode_gqa_attention(L.q, L.kp, L.vp, attended, slot_ids, bt, num_programs=splits)
+        return f
+
+    # parity spot check of layer 0 against the oracle before timing
+    call(0)()
+    torch.cuda.synchronize()
+    kp0, vp0 = case.appended_pools()
+    want = ref.decode_attention(case.q, kp0, vp0, case.attended, case.slot_ids, case.block_table)
+    err = (outs[0][0].float().cpu() - want).abs().max().item()
+    pool_ok = torch.equal(layers[0].kp.cpu().view(torch.int16), kp0.view(torch.int16))
+    log(f"parity: max abs err {err:.2e}, append bit-exact {pool_ok}")
+    if err > 2e-3 or not pool_ok:
+        raise SystemExit(f"parity check failed (err {err}, append exact {pool_ok})")
+
+    use_graph = not args.no_graph
+    us_call, steps = time_calls([call(i) for i in range(R)], args.steps, args.warmup, use_graph, args.repeats)
+    log(f"call (append + decode): {us_call:.2f} us")
+    us_eager, _ = time_calls([call(i) for i in range(R)], max(R, args.steps // 4), R, False, 3)
+    log(f"call, eager launches: {us_eager:.2f} us")
+    us_dec, _ = time_calls([decode_only(i) for i in range(R)], args.steps, args.warmup, use_graph, args.repeats)
+    log(f"decode op alone: {us_dec:.2f} us")
+
+    attended_list = case.attended.tolist()
+    bytes_call = ref.decode_algorithmic_bytes(attended_list, 14, 2, 64, 16)
+    append_bytes = 2 * case.B * 2 * 64 * 2 * 2 + 16 * case.B
+    bytes_dec = bytes_call - append_bytes
+    gbps = bytes_call / (us_call * 1e-6) / 1e9
+    dec_gbps = bytes_dec / (us_dec * 1e-6) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        cpu_us, n_runs, threads, _ = cpu_baseline(case)
+        cpu = {"value": round(bytes_call / (cpu_us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads,
+               "kind": "port", "us_per_call": round(cpu_us, 1),
+               "sample": f"the full headline call (append + decode, B={case.B}, attend "
+                         f"{attended_list[0]}), median of {n_runs} runs after 2 warmups, "
+                         f"{threads} threads on {cpu_model()}"}
+        log(f"cpu baseline: {cpu_us:.0f} us/call on {threads} threads")
+
+    wl = ("paged GQA decode call = KV append + split-KV load + merge, one layer" if args.config == 2
+          else "long-context paged GQA decode call (config 4)")
+    line = {
+        "metric": METRIC,
+        "value": round(gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_call / 1e3, 6),
+        "us_per_call": round(us_call, 3),
+        "pct_of_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1),
+        "us_per_call_eager": round(us_eager, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (fp32 accumulate)",
+        "data": "synthetic (seeded N(0,1)*0.5 pools, shuffled pages)",
+        "config": {
+            "workload": wl,
+            "config_id": args.config,
+            "batch": case.B,
+            "kv_len_prior": int(case.kv_lens[0]),
+            "attended": attended_list[0],
+            "heads_q": 14, "heads_kv": 2, "head_dim": 64, "page_size": 16,
+            "pool_pages_per_layer": int(case.k_pool.shape[0]),
+            "layer_rotation": R,
+            "splits": splits or cie.attn.core.default_decode_splits(case.B, 2),
+            "timing": "hipGraph replay of R calls" if use_graph else "eager launches",
+            "algorithmic_bytes_per_call": bytes_call,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode op (paged_decode split + merge kernels)",
+            "achieved": round(dec_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
+            "us_per_launch": round(us_dec, 3),
+            "algorithmic_bytes_per_launch": bytes_dec,
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_mixed(args, cie, inputs, ref, dev):
+    """Config 3 (mixed chunked prefill + decode): us/call of append + mixed attention."""
+    case = inputs.config3(seed=0)
+    c = case.to(dev)
+    pool_bytes = 2 * case.k_pool.numel() * 2
+    R = max(1, -(-MIN_ROTATION_BYTES // pool_bytes))
+    layers = build_layers(case, dev, R)
+    outs = [None] * R
+
+    def call(i):
+        L = layers[i]
+
+        def f():
+            cie.kv_append_tokens(L.kp, L.vp, L.k_new, L.v_new, c.pages, c.offsets)
+            outs[i] = cie.mixed_gqa_attention(L.q, L.kp, L.vp, 256, c.cu_seqlens, c.kv_lens, c.slot_ids,
+                                              c.block_table)
+        return f
+
+    call(0)()
+    torch.cuda.synchronize()
+    want, written = ref.mixed_attention(case.q, *case.appended_pools(), case.cu_seqlens, case.kv_lens,
+                                        case.slot_ids, case.block_table)
+    err = (outs[0][0].float().cpu() - want)[written].abs().max().item()
+    log(f"mixed parity: max abs err {err:.2e}")
+    us, steps = time_calls([call(i) for i in range(R)], args.steps, args.warmup, not args.no_graph,
+                           args.repeats)
+    E = (case.kv_lens + case.new_lens).tolist()
+    kv_bytes = 2 * sum(E) * 2 * 64 * 2
+    qo = 2 * case.T * 14 * 64 * 2
+    app = 2 * case.T * 2 * 64 * 2 * 2
+    nbytes = kv_bytes + qo + app
+    flops = 0
+    for cc, L in zip(case.kv_lens.tolist(), case.new_lens.tolist()):
+        keys = sum(cc + i + 1 for i in range(L))
+        flops += 4 * 14 * 64 * keys
+    print(json.dumps({
+        "metric": "mixed varlen chunked prefill + decode us/call (config 3)",
+        "value": round(us, 3), "unit": "us/call", "higher_is_better": False, "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6),
+        "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+        "achieved_TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
+        "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
+        "config": {"workload": "config 3 mixed: 4x256-row prefill chunks + 28 decode rows", "T": case.T,
+                   "algorithmic_bytes": nbytes, "flops": flops, "layer_rotation": R},
+        "parity_max_abs_err": err,
+    }), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,267 @@
+"""Paged GQA attention host functions, ``torch.library`` ops and the Qwen2 drop-in.
+
+Same surface as the reference's attn/core.py:
+  * ``decode_gqa_attention`` (attn/core.py:13-66) — split-KV decode, one query
+    token per sequence; ``num_programs`` is the KV split count.
+  * ``mixed_gqa_attention`` (attn/core.py:69-111) — varlen causal attention for
+    packed chunked-prefill + decode batches.
+  * ops ``inference::gqa_decode_attention`` / ``inference::gqa_mixed_attention``
+    (attn/core.py:119-137): functional (``mutates_args=()``), with fake impls so
+    ``torch.compile(fullgraph=True)`` traces through them.
+  * ``TritonQwen2Attention`` / ``replace_attention`` / ``use_triton_attention``
+    (attn/core.py:139-250).  The class keeps the reference's name so callers
+    switch by import; it runs the gfx950 HIP kernels, not Triton.
+
+The Triton launch knobs (``BLOCK_N``, ``BLOCK_M``, ``num_warps``, ``wrap``) are
+accepted and ignored.  Validation mirrors the reference's asserts and raises
+``AssertionError`` with the same conditions (never stripped by ``-O``).
+Outputs and split workspaces are allocated with ``torch.empty`` on the
+current stream, so under graph capture they come from the graph pool.
+"""
+from __future__ import annotations
+
+import torch
+from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention, apply_rotary_pos_emb
+
+from .. import _native
+
+# Decode kernel geometry: waves per workgroup of the split kernel.
+DECODE_WAVES_PER_SPLIT = 4
+# Target resident wavefronts for the split grid (256 CUs x 16 waves).
+DECODE_TARGET_WAVES = 4096
+DECODE_MAX_SPLITS = 64
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise AssertionError(msg)
+
+
+def _index(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.int64 or not t.is_contiguous():
+        t = t.to(torch.int64).contiguous()
+    return t
+
+
+def _block_table(bt: torch.Tensor) -> torch.Tensor:
+    if bt.dtype != torch.int64 or bt.stride(1) != 1:
+        bt = bt.to(torch.int64).contiguous()
+    return bt
+
+
+def default_decode_splits(batch: int, h_kv: int) -> int:
+    """Split count that puts about DECODE_TARGET_WAVES waves on the chip."""
+    units = max(1, batch * h_kv * DECODE_WAVES_PER_SPLIT)
+    return max(1, min(DECODE_MAX_SPLITS, -(-DECODE_TARGET_WAVES // units)))
+
+
+def _check_pool(q, k, v):
+    _require(k.dim() == 4 and k.shape == v.shape, "K/V pools must be (n_pages, H_kv, page_size, D)")
+    _require(
+        k.stride() == v.stride() and k.stride(3) == 1 and k.stride(2) == q.shape[-1],
+        "K/V pools need identical strides with dense (page_size, D) rows",
+    )
+    _require(q.dtype == torch.float16 and k.dtype == torch.float16 and v.dtype == torch.float16,
+             "q and the K/V pools must be float16")
+
+
+def decode_gqa_attention(q, k, v, lens, slot_ids, block_table, num_programs=None,
+                         BLOCK_N=64, num_warps=4, wrap=None, err=None):
+    """Paged GQA decode: ``o[0, b, h] = softmax(q[0, b, h] K^T / sqrt(D)) V`` over ``lens[b]`` tokens.
+
+    q: (1, B, H_q, D) fp16 contiguous; k, v: (n_pages, H_kv, page_size, D);
+    lens (B,) = attended lengths; slot_ids (B,); block_table (n_slots, n_pages).
+    """
+    total_T, H_q, D = q.shape[1:]
+    N_PAGES, H_kv, PAGE_SIZE, _ = k.shape
+    B = slot_ids.shape[0]
+    _require(H_q % H_kv == 0, "H_q must be a multiple of H_kv")
+    _require(tuple(lens.shape) == (B,), "lens must be (B,)")
+    _require(N_PAGES == block_table.shape[1], "block_table width must equal n_pages")
+    _require(total_T == B, "decode takes one query token per sequence")
+    _require(q.is_contiguous(), "q must be contiguous")
+    _check_pool(q, k, v)
+    dev = _native.require_device(q, k, v, lens, slot_ids, block_table)
+    lens, slot_ids, block_table = _index(lens), _index(slot_ids), _block_table(block_table)
+    P = int(num_programs) if num_programs else default_decode_splits(B, H_kv)
+    _require(P >= 1, "num_programs must be >= 1")
+
+    lib = _native.load()
+    o = torch.empty_like(q)
+    if B == 0:
+        return o
+    ws = torch.empty(lib.cie_paged_decode_workspace_bytes(B, H_q, D, P), dtype=torch.uint8, device=dev)
+    _native.check(
+        lib.cie_paged_decode(
+            o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            lens.data_ptr(), slot_ids.data_ptr(), block_table.data_ptr(), ws.data_ptr(),
+            B, H_q, H_kv, D, PAGE_SIZE, N_PAGES, k.stride(0), k.stride(1),
+            block_table.stride(0), block_table.shape[1], block_table.shape[0], P,
+            _native.ptr(err), _native.stream_handle(dev),
+        ),
+        "cie_paged_decode",
+    )
+    return o
+
+
+def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids, block_table,
+                        BLOCK_M=16, BLOCK_N=64, num_warps=4, wrap=None, err=None):
+    """Varlen causal GQA attention over the paged pool (chunked prefill + decode).
+
+    q: (1, total_T, H_q, D) fp16 contiguous; cu_seqlens (B+1,); kv_lens (B,) =
+    prior lengths; row i of sequence b attends keys [0, kv_lens[b] + i].
+    Rows outside every sequence are left as ``torch.empty_like`` leaves them.
+    """
+    total_T, H_q, D = q.shape[1:]
+    N_PAGES, H_kv, PAGE_SIZE, _ = k.shape
+    B = slot_ids.shape[0]
+    _require(H_q % H_kv == 0, "H_q must be a multiple of H_kv")
+    _require(tuple(kv_lens.shape) == (B,), "kv_lens must be (B,)")
+    _require(tuple(cu_seqlens.shape) == (B + 1,), "cu_seqlens must be (B+1,)")
+    _require(N_PAGES == block_table.shape[1], "block_table width must equal n_pages")
+    _require(q.is_contiguous() and k.is_contiguous() and v.is_contiguous(), "q, k, v must be contiguous")
+    _check_pool(q, k, v)
+    dev = _native.require_device(q, k, v, cu_seqlens, kv_lens, slot_ids, block_table)
+    cu_seqlens, kv_lens, slot_ids = _index(cu_seqlens), _index(kv_lens), _index(slot_ids)
+    block_table = _block_table(block_table)
+
+    lib = _native.load()
+    o = torch.empty_like(q)
+    if B == 0 or total_T == 0 or int(max_seqlen) == 0:
+        return o
+    ws = torch.empty(lib.cie_mixed_workspace_bytes(B, H_kv, D), dtype=torch.uint8, device=dev)
+    _native.check(
+        lib.cie_mixed_attention(
+            o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            cu_seqlens.data_ptr(), kv_lens.data_ptr(), slot_ids.data_ptr(), block_table.data_ptr(),
+            ws.data_ptr(), B, total_T, int(max_seqlen), H_q, H_kv, D, PAGE_SIZE, N_PAGES,
+            k.stride(0), k.stride(1), block_table.stride(0), block_table.shape[1],
+            block_table.shape[0], _native.ptr(err), _native.stream_handle(dev),
+        ),
+        "cie_mixed_attention",
+    )
+    return o
+
+
+# Op-level configs (the reference's GQA_DECODE_CONFIG / GQA_PREFILL_CONFIG,
+# attn/core.py:114-116).  num_programs=None picks the split count per batch.
+GQA_DECODE_CONFIG = {"num_programs": None}
+GQA_PREFILL_CONFIG = {}
+
+
+@torch.library.custom_op("inference::gqa_decode_attention", mutates_args=())
+def gqa_decode_attention_op(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+    lens: torch.Tensor, slot_ids: torch.Tensor, block_table: torch.Tensor,
+) -> torch.Tensor:
+    return decode_gqa_attention(q, k, v, lens=lens, slot_ids=slot_ids, block_table=block_table,
+                                **GQA_DECODE_CONFIG)
+
+
+@gqa_decode_attention_op.register_fake
+def _(q, k, v, lens, slot_ids, block_table):
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("inference::gqa_mixed_attention", mutates_args=())
+def gqa_mixed_attention_op(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+    max_seqlen: int, cu_seqlens: torch.Tensor, kv_lens: torch.Tensor,
+    slot_ids: torch.Tensor, block_table: torch.Tensor,
+) -> torch.Tensor:
+    return mixed_gqa_attention(q, k, v, **GQA_PREFILL_CONFIG, max_seqlen=max_seqlen,
+                               cu_seqlens=cu_seqlens, block_table=block_table, kv_lens=kv_lens,
+                               slot_ids=slot_ids)
+
+
+@gqa_mixed_attention_op.register_fake
+def _(q, k, v, max_seqlen, cu_seqlens, kv_lens, slot_ids, block_table):
+    return torch.empty_like(q)
+
+
+class TritonQwen2Attention(torch.nn.Module):
+    """Drop-in for HF ``Qwen2Attention`` over the paged pool (attn/core.py:139-236).
+
+    Fused QKV projection -> RoPE -> KV append (decode or token mode) -> paged
+    attention (decode or mixed) -> o_proj.  Falls back to the wrapped HF module
+    when no ``kv_manager`` is passed.
+    """
+
+    def __init__(self, original_attn):
+        super().__init__()
+        if original_attn.sliding_window is not None:
+            raise AssertionError("sliding window attention is not supported")
+        self.original = original_attn
+        self.layer_idx = original_attn.layer_idx
+        self.num_heads = original_attn.config.num_attention_heads
+        self.head_dim = original_attn.head_dim
+        if original_attn.scaling != self.head_dim ** -0.5:
+            raise AssertionError("only the default 1/sqrt(head_dim) scaling is supported")
+        projs = [original_attn.q_proj, original_attn.k_proj, original_attn.v_proj]
+        if not all(p.bias is not None for p in projs):
+            raise AssertionError("q/k/v projections must have biases")
+        self.qkv_sizes = [p.out_features for p in projs]
+        with torch.no_grad():
+            self.register_buffer("qkv_weight", torch.cat([p.weight for p in projs]), persistent=False)
+            self.register_buffer("qkv_bias", torch.cat([p.bias for p in projs]), persistent=False)
+        self.fuse_qkv = True
+
+    def forward(self, hidden_states, position_embeddings, attention_mask=None,
+                past_key_values=None, kv_manager=None, **kwargs):
+        if kv_manager is None:
+            return self.original(hidden_states, position_embeddings, attention_mask,
+                                 past_key_values=past_key_values, **kwargs)
+        metadata = kwargs.get("metadata")
+        if metadata is None:
+            raise ValueError("'metadata' is required with custom kv_manager.")
+
+        attn = self.original
+        total_T = hidden_states.shape[1]
+        hidden_shape = (1, total_T, -1, self.head_dim)
+        if self.fuse_qkv:
+            q, k, v = torch.nn.functional.linear(hidden_states, self.qkv_weight, self.qkv_bias).split(
+                self.qkv_sizes, dim=-1)
+        else:
+            q, k, v = attn.q_proj(hidden_states), attn.k_proj(hidden_states), attn.v_proj(hidden_states)
+        query_states = q.view(hidden_shape)
+        key_states = k.view(hidden_shape)
+        value_states = v.view(hidden_shape)
+        cos, sin = position_embeddings
+        query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin,
+                                                        unsqueeze_dim=2)
+
+        if metadata.full_decode:
+            kv_manager.decode_update(self.layer_idx, metadata.slot_ids, key_states, value_states)
+            o = gqa_decode_attention_op(
+                query_states, kv_manager.keys[self.layer_idx], kv_manager.values[self.layer_idx],
+                kv_manager.lens[metadata.slot_ids] + 1,
+                slot_ids=metadata.slot_ids, block_table=kv_manager.block_table,
+            )
+        else:
+            kv_manager.mixed_update(self.layer_idx, metadata.pages, metadata.offsets,
+                                    key_states, value_states)
+            o = gqa_mixed_attention_op(
+                query_states, kv_manager.keys[self.layer_idx], kv_manager.values[self.layer_idx],
+                kv_lens=kv_manager.lens[metadata.slot_ids], max_seqlen=metadata.max_seqlen,
+                cu_seqlens=metadata.cu_seqlens, slot_ids=metadata.slot_ids,
+                block_table=kv_manager.block_table,
+            )
+        attn_output = attn.o_proj(o.reshape(1, total_T, self.num_heads * self.head_dim))
+        return attn_output, None
+
+
+HipQwen2Attention = TritonQwen2Attention
+
+
+def replace_attention(module) -> None:
+    for name, child in module.named_children():
+        if isinstance(child, Qwen2Attention):
+            setattr(module, name, TritonQwen2Attention(child))
+        elif not isinstance(child, TritonQwen2Attention):
+            replace_attention(child)
+
+
+def use_triton_attention(model) -> None:
+    if not getattr(model, "_uses_triton_attention", False):
+        replace_attention(model)
+        model._uses_triton_attention = True

@@ -1,0 +1,194 @@
+// KV append into the paged pool: the new tokens' K/V rows are scattered into
+// (page, in-page offset) slots of the (n_pages, H_kv, page_size, D) pools.
+//
+// One launch covers K and V of every (token, kv head).  A lane moves one
+// VEC-wide chunk of one row for both K and V, lanes of a row are adjacent, so
+// the reads of k_new/v_new and the 2*D-byte row writes into the pool are
+// coalesced.  The copy is a pure fp16 move: bit-exact by construction.
+//
+// Decode mode follows KVStorage.decode_update (kv_cache/storage.py:87-122):
+//   pos = lens[slot]; page = block_table[slot, pos // page_size];
+//   off = pos % page_size.
+// Token mode follows KVStorage.mixed_update (kv_cache/storage.py:62-85):
+//   page = pages[t]; off = offsets[t].
+#include "cie_common.h"
+
+namespace cie {
+
+struct AppendParams {
+  f16* k_pool;
+  f16* v_pool;
+  const f16* k_new;
+  const f16* v_new;
+  int64_t k_tok_stride, k_head_stride, v_tok_stride, v_head_stride;
+  // decode mode
+  const int64_t* slot_ids;
+  const int64_t* lens;
+  const int64_t* block_table;
+  int64_t bt_stride;
+  int64_t bt_width;
+  int64_t n_slots;
+  // token mode
+  const int64_t* pages;
+  const int64_t* offsets;
+  // common
+  int64_t n_rows;  // B (decode) or T (tokens)
+  int64_t n_pages;
+  int64_t pool_page_stride, pool_head_stride;
+  int32_t H_kv, page_size, D;
+  int32_t* err;
+};
+
+template <int VEC, bool kDecode>
+__global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
+  typedef f16 vec_t __attribute__((ext_vector_type(VEC)));
+  const int chunks = p.D / VEC;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = p.n_rows * p.H_kv * chunks;
+  if (gid >= total) return;
+  const int c = (int)(gid % chunks);
+  const int h = (int)((gid / chunks) % p.H_kv);
+  const int64_t row = gid / ((int64_t)chunks * p.H_kv);
+
+  int64_t page, off;
+  if constexpr (kDecode) {
+    const int64_t slot = p.slot_ids[row];
+    if (slot < 0 || slot >= p.n_slots) {
+      set_err(p.err, CIE_ERRBIT_PAGE);
+      return;
+    }
+    const int64_t pos = p.lens[slot];
+    if (pos < 0 || pos >= p.bt_width * p.page_size) {
+      set_err(p.err, CIE_ERRBIT_LEN);
+      return;
+    }
+    page = p.block_table[slot * p.bt_stride + pos / p.page_size];
+    off = pos % p.page_size;
+  } else {
+    page = p.pages[row];
+    off = p.offsets[row];
+    if (off < 0 || off >= p.page_size) {
+      set_err(p.err, CIE_ERRBIT_OFFSET);
+      return;
+    }
+  }
+  if (page < 0 || page >= p.n_pages) {
+    set_err(p.err, CIE_ERRBIT_PAGE);
+    return;
+  }
+
+  const int64_t dst = page * p.pool_page_stride + h * p.pool_head_stride +
+                      off * p.D + (int64_t)c * VEC;
+  const vec_t kv = *reinterpret_cast<const vec_t*>(
+      p.k_new + row * p.k_tok_stride + h * p.k_head_stride + c * VEC);
+  const vec_t vv = *reinterpret_cast<const vec_t*>(
+      p.v_new + row * p.v_tok_stride + h * p.v_head_stride + c * VEC);
+  *reinterpret_cast<vec_t*>(p.k_pool + dst) = kv;
+  *reinterpret_cast<vec_t*>(p.v_pool + dst) = vv;
+}
+
+static bool aligned16(const void* ptr) {
+  return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0;
+}
+
+template <bool kDecode>
+static int launch_append(const AppendParams& p, hipStream_t stream) {
+  if (p.n_rows == 0) return CIE_OK;
+  const bool vec8 = (p.D % 8 == 0) && aligned16(p.k_pool) && aligned16(p.v_pool) &&
+                    aligned16(p.k_new) && aligned16(p.v_new) &&
+                    p.k_tok_stride % 8 == 0 && p.k_head_stride % 8 == 0 &&
+                    p.v_tok_stride % 8 == 0 && p.v_head_stride % 8 == 0 &&
+                    p.pool_page_stride % 8 == 0 && p.pool_head_stride % 8 == 0;
+  const int vec = vec8 ? 8 : 1;
+  const int64_t total = p.n_rows * p.H_kv * (p.D / vec);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffff) return CIE_EUNSUPPORTED;
+  if (vec8)
+    hipLaunchKernelGGL((kv_append_kernel<8, kDecode>), dim3((unsigned)blocks),
+                       dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((kv_append_kernel<1, kDecode>), dim3((unsigned)blocks),
+                       dim3(256), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
+}  // namespace cie
+
+using namespace cie;
+
+extern "C" int cie_kv_append_decode(
+    void* k_pool, void* v_pool, const void* k_new, const void* v_new,
+    int64_t k_tok_stride, int64_t k_head_stride, int64_t v_tok_stride,
+    int64_t v_head_stride, const int64_t* slot_ids, const int64_t* lens,
+    const int64_t* block_table, int64_t B, int64_t H_kv, int64_t page_size,
+    int64_t D, int64_t n_pages, int64_t pool_page_stride,
+    int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
+    int64_t n_slots, int32_t* err, void* stream) {
+  if (B < 0 || H_kv <= 0 || page_size <= 0 || D <= 0 || n_pages <= 0 ||
+      bt_width <= 0 || bt_stride < bt_width || n_slots <= 0)
+    return CIE_EINVAL;
+  if (B > 0 && (!k_pool || !v_pool || !k_new || !v_new || !slot_ids || !lens ||
+                !block_table))
+    return CIE_EINVAL;
+  if (H_kv > 0x7fffffff || page_size > 0x7fffffff || D > 0x7fffffff)
+    return CIE_EUNSUPPORTED;
+  AppendParams p{};
+  p.k_pool = static_cast<f16*>(k_pool);
+  p.v_pool = static_cast<f16*>(v_pool);
+  p.k_new = static_cast<const f16*>(k_new);
+  p.v_new = static_cast<const f16*>(v_new);
+  p.k_tok_stride = k_tok_stride;
+  p.k_head_stride = k_head_stride;
+  p.v_tok_stride = v_tok_stride;
+  p.v_head_stride = v_head_stride;
+  p.slot_ids = slot_ids;
+  p.lens = lens;
+  p.block_table = block_table;
+  p.bt_stride = bt_stride;
+  p.bt_width = bt_width;
+  p.n_slots = n_slots;
+  p.n_rows = B;
+  p.n_pages = n_pages;
+  p.pool_page_stride = pool_page_stride;
+  p.pool_head_stride = pool_head_stride;
+  p.H_kv = (int32_t)H_kv;
+  p.page_size = (int32_t)page_size;
+  p.D = (int32_t)D;
+  p.err = err;
+  return launch_append<true>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cie_kv_append_tokens(
+    void* k_pool, void* v_pool, const void* k_new, const void* v_new,
+    int64_t k_tok_stride, int64_t k_head_stride, int64_t v_tok_stride,
+    int64_t v_head_stride, const int64_t* pages, const int64_t* offsets,
+    int64_t T, int64_t H_kv, int64_t page_size, int64_t D, int64_t n_pages,
+    int64_t pool_page_stride, int64_t pool_head_stride, int32_t* err,
+    void* stream) {
+  if (T < 0 || H_kv <= 0 || page_size <= 0 || D <= 0 || n_pages <= 0)
+    return CIE_EINVAL;
+  if (T > 0 && (!k_pool || !v_pool || !k_new || !v_new || !pages || !offsets))
+    return CIE_EINVAL;
+  if (H_kv > 0x7fffffff || page_size > 0x7fffffff || D > 0x7fffffff)
+    return CIE_EUNSUPPORTED;
+  AppendParams p{};
+  p.k_pool = static_cast<f16*>(k_pool);
+  p.v_pool = static_cast<f16*>(v_pool);
+  p.k_new = static_cast<const f16*>(k_new);
+  p.v_new = static_cast<const f16*>(v_new);
+  p.k_tok_stride = k_tok_stride;
+  p.k_head_stride = k_head_stride;
+  p.v_tok_stride = v_tok_stride;
+  p.v_head_stride = v_head_stride;
+  p.pages = pages;
+  p.offsets = offsets;
+  p.n_rows = T;
+  p.n_pages = n_pages;
+  p.pool_page_stride = pool_page_stride;
+  p.pool_head_stride = pool_head_stride;
+  p.H_kv = (int32_t)H_kv;
+  p.page_size = (int32_t)page_size;
+  p.D = (int32_t)D;
+  p.err = err;
+  return launch_append<false>(p, static_cast<hipStream_t>(stream));
+}

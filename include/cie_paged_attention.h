@@ -1,0 +1,142 @@
+/*
+ * cie_paged_attention.h — C ABI of the MI355X (gfx950) paged-KV GQA attention
+ * hot path: KV append, split-KV decode (load + merge) and the varlen mixed
+ * (chunked prefill + decode) causal kernel.
+ *
+ * Conventions shared by every entry point
+ * ---------------------------------------
+ *  - Every pointer is a device pointer owned by the caller.  Nothing here
+ *    allocates, frees or synchronises; kernels are enqueued on `stream`
+ *    (a hipStream_t passed as void*; NULL = the null stream), so the calls are
+ *    safe under hipGraph stream capture.
+ *  - fp16 tensors are IEEE binary16.  Index tensors are int64, the dtype the
+ *    reference uses for lens / slot ids / block tables / cu_seqlens.
+ *  - KV pool layout is the reference's (n_pages, H_kv, page_size, D) with the
+ *    last two dims dense (stride(3) == 1, stride(2) == D); the page and head
+ *    strides are passed explicitly (in elements).
+ *  - The block table is (n_slots, bt_stride) int64; only the first bt_width
+ *    entries of a row are valid logical pages.
+ *  - `err` (nullable) is an int32 device word.  Kernels never fault on a bad
+ *    index: an out-of-range page id, slot id or length is clamped / skipped and
+ *    the matching CIE_ERRBIT_* bit is OR-ed into *err.
+ *  - Return value: 0 on success, a negative CIE_E* code for an argument error
+ *    detected on the host (nothing is launched), or a positive hipError_t from
+ *    the launch.
+ */
+#ifndef CIE_PAGED_ATTENTION_H
+#define CIE_PAGED_ATTENTION_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CIE_OK 0
+#define CIE_EINVAL (-1)      /* inconsistent sizes / strides / null pointer      */
+#define CIE_EUNSUPPORTED (-2) /* shape outside what the kernels are built for   */
+
+#define CIE_ERRBIT_PAGE 1     /* page id outside [0, n_pages)                    */
+#define CIE_ERRBIT_LEN 2      /* length beyond the block-table row capacity      */
+#define CIE_ERRBIT_OFFSET 4   /* in-page offset outside [0, page_size)           */
+
+/* Version of this ABI (bumped on any signature change). */
+int cie_abi_version(void);
+
+/* Human-readable name of a CIE_E* / hipError_t status. */
+const char* cie_status_string(int status);
+
+/*
+ * Decode KV append: for each sequence b, pos = lens[slot_ids[b]],
+ *   k_pool[block_table[slot, pos / page_size], h, pos % page_size, :] = k_new[b, h, :]
+ * (same for V).  Bit-exact fp16 copy.
+ * Replaces KVStorage.decode_update (kv_cache/storage.py:87-122): the torch
+ * gather of lens / block_table plus two index_put_ scatters.
+ * k_new / v_new are (B, H_kv, D) views with their own token and head strides
+ * (elements); the last dim must be dense.
+ */
+int cie_kv_append_decode(void* k_pool, void* v_pool,
+                         const void* k_new, const void* v_new,
+                         int64_t k_tok_stride, int64_t k_head_stride,
+                         int64_t v_tok_stride, int64_t v_head_stride,
+                         const int64_t* slot_ids, const int64_t* lens,
+                         const int64_t* block_table,
+                         int64_t B, int64_t H_kv, int64_t page_size, int64_t D,
+                         int64_t n_pages, int64_t pool_page_stride,
+                         int64_t pool_head_stride, int64_t bt_stride,
+                         int64_t bt_width, int64_t n_slots,
+                         int32_t* err, void* stream);
+
+/*
+ * Token-mode (mixed) KV append: for each packed token t < T,
+ *   k_pool[pages[t], h, offsets[t], :] = k_new[t, h, :]   (same for V).
+ * Replaces KVStorage.mixed_update (kv_cache/storage.py:62-85).
+ */
+int cie_kv_append_tokens(void* k_pool, void* v_pool,
+                         const void* k_new, const void* v_new,
+                         int64_t k_tok_stride, int64_t k_head_stride,
+                         int64_t v_tok_stride, int64_t v_head_stride,
+                         const int64_t* pages, const int64_t* offsets,
+                         int64_t T, int64_t H_kv, int64_t page_size, int64_t D,
+                         int64_t n_pages, int64_t pool_page_stride,
+                         int64_t pool_head_stride, int32_t* err, void* stream);
+
+/*
+ * Split-KV paged GQA decode, one query token per sequence:
+ *   o[b, h, :] = softmax(q[b, h, :] . K_b^T * D^-0.5) . V_b
+ * over the first lens[b] tokens of slot slot_ids[b]'s pages, kv head h / G.
+ * lens[b] == 0 gives o = 0.
+ * Replaces decode_gqa_attention (attn/core.py:13-66), i.e. the Triton
+ * decode_gqa_attention_kernel_load (kernels/decode_attention.py:12-179) and
+ * decode_attention_kernel_merge (kernels/decode_attention.py:182-272).
+ *   q, o       : (B, H_q, D) dense fp16
+ *   workspace  : cie_paged_decode_workspace_bytes(B, H_q, D, n_splits) bytes,
+ *                any contents (partial softmax state of the splits)
+ *   n_splits   : KV splits per (sequence, kv head) — the reference's
+ *                `num_programs`.
+ */
+int64_t cie_paged_decode_workspace_bytes(int64_t B, int64_t H_q, int64_t D,
+                                         int64_t n_splits);
+int cie_paged_decode(void* o, const void* q,
+                     const void* k_pool, const void* v_pool,
+                     const int64_t* lens, const int64_t* slot_ids,
+                     const int64_t* block_table,
+                     void* workspace,
+                     int64_t B, int64_t H_q, int64_t H_kv, int64_t D,
+                     int64_t page_size, int64_t n_pages,
+                     int64_t pool_page_stride, int64_t pool_head_stride,
+                     int64_t bt_stride, int64_t bt_width, int64_t n_slots,
+                     int64_t n_splits, int32_t* err, void* stream);
+
+/*
+ * Varlen causal GQA attention over the paged pool for a packed batch of
+ * chunked-prefill and decode sequences.  Sequence b owns query rows
+ * [cu_seqlens[b], cu_seqlens[b+1]); its row i sits at absolute position
+ * kv_lens[b] + i and attends keys [0, kv_lens[b] + i] of slot slot_ids[b].
+ * Rows outside every sequence are not written.
+ * Replaces mixed_gqa_attention (attn/core.py:69-111), i.e. the Triton
+ * mixed_gqa_attention_kernel (kernels/prefill_attention.py:10-198).
+ *   q, o       : (total_T, H_q, D) dense fp16
+ *   max_seqlen : upper bound on every sequence's query length (the
+ *                reference's metadata token-count bucket); sizes the grid
+ *   workspace  : cie_mixed_workspace_bytes(B, H_kv, D) bytes, any contents
+ *                (split-KV partial state of short-query sequences)
+ */
+int64_t cie_mixed_workspace_bytes(int64_t B, int64_t H_kv, int64_t D);
+int cie_mixed_attention(void* o, const void* q,
+                        const void* k_pool, const void* v_pool,
+                        const int64_t* cu_seqlens, const int64_t* kv_lens,
+                        const int64_t* slot_ids, const int64_t* block_table,
+                        void* workspace,
+                        int64_t B, int64_t total_T, int64_t max_seqlen,
+                        int64_t H_q, int64_t H_kv, int64_t D,
+                        int64_t page_size, int64_t n_pages,
+                        int64_t pool_page_stride, int64_t pool_head_stride,
+                        int64_t bt_stride, int64_t bt_width, int64_t n_slots,
+                        int32_t* err, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CIE_PAGED_ATTENTION_H */

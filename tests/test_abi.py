@@ -1,0 +1,104 @@
+"""The C-ABI library: it loads, exports every declared symbol, and its host-side
+validation rejects bad arguments before launching anything (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from custom_inference_engine_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cie_paged_attention.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cie_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_hot_path():
+    names = declared_functions()
+    for want in ("cie_kv_append_decode", "cie_kv_append_tokens", "cie_paged_decode",
+                 "cie_paged_decode_workspace_bytes", "cie_mixed_attention",
+                 "cie_mixed_workspace_bytes", "cie_abi_version", "cie_status_string"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol(native_lib):
+    missing = [n for n in declared_functions() if not hasattr(native_lib, n)]
+    assert not missing, missing
+    # and the ctypes table covers the same set, so every entry point is typed
+    assert set(_native._SIGNATURES) == set(declared_functions())
+
+
+def test_single_hip_runtime_in_process(native_lib):
+    """The library binds to torch's HIP runtime (one libamdhip64 mapping)."""
+    maps = open("/proc/self/maps").read()
+    paths = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(paths) == 1, paths
+
+
+def test_version_and_status_strings(native_lib):
+    assert native_lib.cie_abi_version() == _native.ABI_VERSION
+    assert native_lib.cie_status_string(0) == b"ok"
+    assert b"invalid" in native_lib.cie_status_string(-1)
+    assert b"unsupported" in native_lib.cie_status_string(-2)
+
+
+def test_workspace_sizes(native_lib):
+    # (B, H_q, S, D + 2) fp32 partial state
+    assert native_lib.cie_paged_decode_workspace_bytes(32, 14, 64, 16) == 32 * 14 * 16 * 66 * 4
+    assert native_lib.cie_paged_decode_workspace_bytes(-1, 14, 64, 16) == -1
+    assert native_lib.cie_mixed_workspace_bytes(32, 2, 64) > 0
+    assert native_lib.cie_mixed_workspace_bytes(32, 0, 64) == -1
+
+
+def _decode_args(**over):
+    a = dict(o=8, q=16, k=32, v=48, lens=64, slots=80, bt=96, ws=112, B=1, H_q=14, H_kv=2, D=64,
+             page_size=16, n_pages=64, page_stride=2048, head_stride=1024, bt_stride=64,
+             bt_width=64, n_slots=2, n_splits=4)
+    a.update(over)
+    return a
+
+
+def _call_decode(lib, a):
+    # fake, never-dereferenced device addresses: these calls must fail validation on the host
+    return lib.cie_paged_decode(a["o"], a["q"], a["k"], a["v"], a["lens"], a["slots"], a["bt"],
+                                a["ws"], a["B"], a["H_q"], a["H_kv"], a["D"], a["page_size"],
+                                a["n_pages"], a["page_stride"], a["head_stride"], a["bt_stride"],
+                                a["bt_width"], a["n_slots"], a["n_splits"], None, None)
+
+
+@pytest.mark.parametrize("over,code", [
+    ({"H_q": 13}, -1),                 # H_q not a multiple of H_kv
+    ({"n_splits": 0}, -1),
+    ({"bt_stride": 8}, -1),            # stride below width
+    ({"page_size": 8}, -2),            # pages must hold whole 16-key tiles
+    ({"D": 96}, -2),                   # head_dim outside the built set
+    ({"H_q": 34, "H_kv": 2}, -2),      # more than 16 query heads per kv head
+    ({"q": 18}, -1),                   # q not 16-byte aligned
+    ({"lens": 0}, -1),                 # null index pointer
+])
+def test_decode_rejects_bad_arguments_without_launching(native_lib, over, code):
+    assert _call_decode(native_lib, _decode_args(**over)) == code
+
+
+def test_decode_empty_batch_is_a_noop(native_lib):
+    assert _call_decode(native_lib, _decode_args(B=0)) == 0
+
+
+def test_append_and_mixed_reject_bad_arguments(native_lib):
+    lib = native_lib
+    # negative row count
+    assert lib.cie_kv_append_tokens(8, 8, 8, 8, 64, 64, 64, 64, 8, 8, -1, 2, 16, 64, 10, 2048,
+                                    1024, None, None) == -1
+    # zero rows: nothing to do
+    assert lib.cie_kv_append_tokens(8, 8, 8, 8, 64, 64, 64, 64, 8, 8, 0, 2, 16, 64, 10, 2048,
+                                    1024, None, None) == 0
+    assert lib.cie_kv_append_decode(8, 8, 8, 8, 64, 64, 64, 64, 8, 8, 8, 1, 2, 16, 64, 10, 2048,
+                                    1024, 4, 8, 2, None, None) == -1  # bt_stride < bt_width
+    # mixed: G = 14 > 8 is outside the built set
+    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, 1, 4, 4, 14, 1, 64, 16, 10,
+                                   1024, 1024, 10, 10, 2, None, None) == -2

@@ -1,0 +1,114 @@
+"""Split-KV paged decode on the GPU against the fp32 oracle (tolerance 2e-3 abs / 1e-2 rel)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from custom_inference_engine_amd import decode_gqa_attention
+from oracle import inputs
+from tests.conftest import assert_attn_close
+from tests.golden.make_golden import INPUT_FIELDS, build_case, digest
+from tests.gpu_helpers import DEV, bits, err_word, gpu_decode_step, note, oracle_decode
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.mark.parametrize("name", ["config1_decode", "decode_edges"])
+def test_decode_matches_golden_fixture(native_lib, name):
+    z = np.load(os.path.join(GOLDEN, f"{name}.npz"), allow_pickle=False)
+    meta = json.loads(str(z["meta"]))
+    case = build_case(meta["spec"])
+    for f in INPUT_FIELDS:
+        assert digest(getattr(case, f)) == meta["digests"][f], f
+    note(f"golden {name}")
+    kp, vp, o = gpu_decode_step(case, n_splits=case.meta.get("n_splits"))
+    assert digest(kp) == meta["pool_digest_k"] and digest(vp) == meta["pool_digest_v"]
+    assert_attn_close(o, torch.from_numpy(z["out"]), what=name)
+
+
+@pytest.mark.parametrize("make,splits", [
+    (lambda: inputs.config1(), 4),
+    (lambda: inputs.config2(seed=0), None),
+    (lambda: inputs.config2(seed=0), 16),
+    (lambda: inputs.config2(seed=1, fixed=False), None),
+    (lambda: inputs.config2(seed=2, fixed=False), 16),
+    (lambda: inputs.config4(), 16),
+], ids=["cfg1-p4", "cfg2-auto", "cfg2-p16", "cfg2var-auto", "cfg2var-p16", "cfg4-p16"])
+def test_decode_baseline_configs(native_lib, make, splits):
+    case = make()
+    note(f"decode B={case.B} max_len={int(case.attended.max())} splits={splits}")
+    kp, vp, o = gpu_decode_step(case, n_splits=splits)
+    ko, vo = case.appended_pools()
+    assert torch.equal(bits(kp), bits(ko)) and torch.equal(bits(vp), bits(vo))
+    assert_attn_close(o, oracle_decode(case), what="decode")
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 16, 64])
+def test_decode_split_count_does_not_change_result(native_lib, splits):
+    case = inputs.make_case([0, 1, 17, 250, 1000], seed=21)
+    note(f"decode split sweep {splits}")
+    _, _, o = gpu_decode_step(case, n_splits=splits)
+    assert_attn_close(o, oracle_decode(case), what=f"splits={splits}")
+
+
+def test_decode_edge_lengths(native_lib):
+    """Attended lengths at and around tile / pair / page boundaries, and zero."""
+    prior = [0, 1, 14, 15, 16, 30, 31, 32, 33, 47, 63, 64, 65, 127, 128]
+    case = inputs.make_case(prior, seed=22)
+    note("decode edges")
+    _, _, o = gpu_decode_step(case, n_splits=3)
+    assert_attn_close(o, oracle_decode(case), what="edges")
+    # an empty sequence gives exactly 0 (kernels/decode_attention.py:260-264)
+    c = case.to(DEV)
+    lens = c.attended.clone()
+    lens[2] = 0
+    out = decode_gqa_attention(c.q, c.k_pool, c.v_pool, lens, c.slot_ids, c.block_table, num_programs=5)
+    assert torch.count_nonzero(out[0, 2]) == 0
+    # one token: o = v of that token (up to fp16 rounding of the output)
+    lens[3] = 1
+    out = decode_gqa_attention(c.q, c.k_pool, c.v_pool, lens, c.slot_ids, c.block_table, num_programs=5)
+    v0 = case.v_pool[case.block_table[4, 0], :, 0].float().repeat_interleave(7, dim=0)
+    assert torch.equal(out[0, 3].float().cpu(), v0.half().float())
+
+
+@pytest.mark.parametrize("h_q,h_kv,d,ps", [
+    (8, 8, 64, 16), (16, 1, 64, 16), (28, 4, 64, 16), (14, 2, 128, 16), (14, 2, 64, 64), (7, 1, 64, 32),
+])
+def test_decode_head_geometries(native_lib, h_q, h_kv, d, ps):
+    case = inputs.make_case([5, 100, 333], seed=23, h_q=h_q, h_kv=h_kv, d=d, page_size=ps)
+    note(f"decode geometry {h_q}/{h_kv} D={d} ps={ps}")
+    kp, vp, o = gpu_decode_step(case, n_splits=4)
+    ko, vo = case.appended_pools()
+    assert torch.equal(bits(kp), bits(ko))
+    assert_attn_close(o, oracle_decode(case), what="geometry")
+
+
+def test_decode_is_deterministic(native_lib):
+    case = inputs.make_case([700, 64, 3000], seed=24)
+    note("decode determinism")
+    o1 = gpu_decode_step(case)[2]
+    o2 = gpu_decode_step(case)[2]
+    assert torch.equal(o1, o2)
+
+
+def test_decode_length_overflow_is_clamped_and_flagged(native_lib):
+    case = inputs.make_case([40], seed=25, bt_width=None)
+    note("decode overflow flag")
+    c = case.to(DEV)
+    err = err_word()
+    cap = c.block_table.shape[1] * 16
+    lens = torch.tensor([cap + 100], device=DEV)
+    decode_gqa_attention(c.q, c.k_pool, c.v_pool, lens, c.slot_ids, c.block_table, num_programs=2, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 2
+
+
+def test_decode_rejects_cpu_tensors():
+    """No CPU fallback: the product path raises on host tensors."""
+    case = inputs.make_case([10], seed=26)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        decode_gqa_attention(case.q, case.k_pool, case.v_pool, case.attended, case.slot_ids,
+                             case.block_table, num_programs=2)

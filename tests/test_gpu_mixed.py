@@ -1,0 +1,110 @@
+"""Varlen mixed (chunked prefill + decode) causal attention on the GPU against the fp32 oracle."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from custom_inference_engine_amd import _native, decode_gqa_attention
+from oracle import inputs
+from tests.conftest import assert_attn_close
+from tests.golden.make_golden import INPUT_FIELDS, build_case, digest
+from tests.gpu_helpers import DEV, bits, err_word, gpu_mixed_step, note, oracle_mixed
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _check(case, o, what):
+    want, written = oracle_mixed(case)
+    assert_attn_close(o[written], want[written], what=what)
+
+
+def test_mixed_matches_golden_fixture(native_lib):
+    z = np.load(os.path.join(GOLDEN, "mixed_small.npz"), allow_pickle=False)
+    meta = json.loads(str(z["meta"]))
+    case = build_case(meta["spec"])
+    for f in INPUT_FIELDS:
+        assert digest(getattr(case, f)) == meta["digests"][f], f
+    note("golden mixed_small")
+    kp, vp, o = gpu_mixed_step(case)
+    assert digest(kp) == meta["pool_digest_k"] and digest(vp) == meta["pool_digest_v"]
+    w = torch.from_numpy(z["written"])
+    assert_attn_close(o[w], torch.from_numpy(z["out"])[w], what="mixed_small")
+
+
+def test_mixed_config3(native_lib):
+    case = inputs.config3()
+    note(f"mixed config3 T={case.T}")
+    kp, vp, o = gpu_mixed_step(case, max_seqlen=case.meta["max_seqlen"])
+    ko, vo = case.appended_pools()
+    assert torch.equal(bits(kp), bits(ko)) and torch.equal(bits(vp), bits(vo))
+    _check(case, o, "config3")
+
+
+@pytest.mark.parametrize("prior,new", [
+    ([0], [1]), ([0], [2]), ([0], [3]), ([0], [16]), ([0], [17]), ([0], [100]),
+    ([0, 0, 0], [31, 32, 33]),
+    ([5, 700, 16, 2000], [1, 1, 2, 1]),              # decode-like (key-parallel) tiles
+    ([100, 0, 3000, 50], [40, 1, 18, 2]),            # prefill tails of 2 and 8 rows
+    ([0, 1500, 0, 64], [250, 3, 0, 129]),            # an empty sequence in the middle
+], ids=lambda x: str(x))
+def test_mixed_shapes(native_lib, prior, new):
+    case = inputs.make_case(prior, new, seed=31)
+    note(f"mixed prior={prior} new={new}")
+    kp, vp, o = gpu_mixed_step(case)
+    ko, vo = case.appended_pools()
+    assert torch.equal(bits(kp), bits(ko)) and torch.equal(bits(vp), bits(vo))
+    _check(case, o, f"mixed {prior}/{new}")
+
+
+def test_mixed_single_rows_match_decode_kernel(native_lib):
+    """L = 1 sequences through the mixed kernel equal the decode kernel on the same pool."""
+    case = inputs.make_case([0, 31, 512, 3071], seed=32)
+    note("mixed vs decode")
+    kp, vp, om = gpu_mixed_step(case)
+    c = case.to(DEV)
+    od = decode_gqa_attention(c.q, kp.to(DEV), vp.to(DEV), c.attended, c.slot_ids, c.block_table)
+    assert_attn_close(om, od[0].float().cpu(), atol=1e-3, rtol=1e-2, what="mixed L=1 vs decode")
+
+
+@pytest.mark.parametrize("h_q,h_kv,d,ps", [(8, 8, 64, 16), (8, 1, 64, 16), (14, 2, 128, 16), (14, 2, 64, 32)])
+def test_mixed_head_geometries(native_lib, h_q, h_kv, d, ps):
+    case = inputs.make_case([0, 40, 300], [37, 1, 20], seed=33, h_q=h_q, h_kv=h_kv, d=d, page_size=ps)
+    note(f"mixed geometry {h_q}/{h_kv} D={d} ps={ps}")
+    _, _, o = gpu_mixed_step(case)
+    _check(case, o, "geometry")
+
+
+def test_mixed_leaves_rows_outside_sequences_untouched(native_lib):
+    """Rows past cu_seqlens[-1] keep their contents (the reference never stores them)."""
+    case = inputs.make_case([10, 0], [5, 3], seed=34)
+    note("mixed untouched rows")
+    c = case.to(DEV)
+    kp, vp = case.appended_pools()
+    kp, vp = kp.to(DEV), vp.to(DEV)
+    T_pad = case.T + 4
+    q = torch.zeros(1, T_pad, 14, 64, dtype=torch.float16, device=DEV)
+    q[:, :case.T] = c.q
+    o = torch.full_like(q, 7.0)
+    lib = _native.load()
+    ws = torch.empty(lib.cie_mixed_workspace_bytes(case.B, 2, 64), dtype=torch.uint8, device=DEV)
+    rc = lib.cie_mixed_attention(o.data_ptr(), q.data_ptr(), kp.data_ptr(), vp.data_ptr(),
+                                 c.cu_seqlens.data_ptr(), c.kv_lens.data_ptr(), c.slot_ids.data_ptr(),
+                                 c.block_table.data_ptr(), ws.data_ptr(), case.B, T_pad, 16, 14, 2, 64,
+                                 16, kp.shape[0], kp.stride(0), kp.stride(1), c.block_table.stride(0),
+                                 c.block_table.shape[1], c.block_table.shape[0], None,
+                                 _native.stream_handle(torch.device(DEV)))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.all(o[0, case.T:] == 7.0)
+    _check(case, o[0, :case.T].float().cpu(), "untouched")
+
+
+def test_mixed_rows_beyond_max_seqlen_are_flagged(native_lib):
+    case = inputs.make_case([0], [40], seed=35)
+    note("mixed max_seqlen flag")
+    err = err_word()
+    gpu_mixed_step(case, max_seqlen=16, err=err)
+    assert int(err.item()) & 2
