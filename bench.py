@@ -8,9 +8,10 @@ Infinity Cache cannot serve repeat reads.  Calls are captured in a hipGraph
 (R calls per graph, as a decode step walks the layers) and replayed.
 
 Prints ONE JSON line.  ``value`` = algorithmic GB/s of a call (higher is
-better); ``us_per_call`` is the same measurement as a time.  ``roofline`` rates
-the dominant kernel(s) (the decode op, timed alone with HIP events on the
-stream it runs on) against 8 TB/s.  ``cpu_baseline`` times the CPU oracle
+better); ``us_per_call`` is the same measurement as a time.  A call is one
+kernel launch (the KV append fused into the decode), so ``roofline`` rates that
+kernel: its per-launch time from HIP events on the stream it runs on, against
+8 TB/s.  The two-launch path (append kernel + decode op) is timed beside it.  ``cpu_baseline`` times the CPU oracle
 (the reference's semantics: torch gather + SDPA in fp32, numpy append) on
 this host on a bounded sample of the same workload.
 
@@ -142,6 +143,33 @@ def cpu_baseline(case, budget_s: float = 20.0, max_runs: int = 7):
     return statistics.median(runs) * 1e6, len(runs), torch.get_num_threads(), out
 
 
+def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chunk: int = 2048):
+    """HBM ceiling of the paged access pattern on this box: the probe kernel reads
+    the same byte volume as one decode call as shuffled chunk-sized pieces of a
+    1 GiB region (R disjoint chunk lists rotate, so the 256 MB MALL cannot help)."""
+    from custom_inference_engine_amd import _native
+
+    lib = _native.load()
+    region = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    n_region = region.numel() // chunk
+    n = nbytes // chunk
+    R = max(1, min(8, n_region // n))
+    perm = torch.randperm(n_region, generator=torch.Generator().manual_seed(7))
+    lists = [perm[i * n:(i + 1) * n].to(torch.int32).to(dev) for i in range(R)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def f(i):
+        def g():
+            _native.check(lib.cie_probe_gather_read(region.data_ptr(), lists[i].data_ptr(), n, chunk, 2048,
+                                                    sink.data_ptr(), _native.stream_handle(dev)),
+                          "cie_probe_gather_read")
+        return g
+
+    us, _ = time_calls([f(i) for i in range(R)], steps, warmup, True, repeats)
+    del region
+    return us, n * chunk
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -198,7 +226,15 @@ def main():
 
     outs = [None] * R
 
-    def call(i):
+    def call_fused(i):
+        L = layers[i]
+
+        def f():
+            outs[i] = cie.decode_append_gqa_attention(L.q, L.kp, L.vp, L.k_new, L.v_new, lens_pool,
+                                                      slot_ids, bt, num_programs=splits)
+        return f
+
+    def call_two_launch(i):
         L = layers[i]
 
         def f():
@@ -213,31 +249,39 @@ def main():
             outs[i] = cie.decode_gqa_attention(L.q, L.kp, L.vp, attended, slot_ids, bt, num_programs=splits)
         return f
 
-    # parity spot check of layer 0 against the oracle before timing
-    call(0)()
-    torch.cuda.synchronize()
+    # parity spot check of layer 0 (both paths) against the oracle before timing
     kp0, vp0 = case.appended_pools()
     want = ref.decode_attention(case.q, kp0, vp0, case.attended, case.slot_ids, case.block_table)
-    err = (outs[0][0].float().cpu() - want).abs().max().item()
-    pool_ok = torch.equal(layers[0].kp.cpu().view(torch.int16), kp0.view(torch.int16))
-    log(f"parity: max abs err {err:.2e}, append bit-exact {pool_ok}")
-    if err > 2e-3 or not pool_ok:
-        raise SystemExit(f"parity check failed (err {err}, append exact {pool_ok})")
+    for name, mk in (("fused", call_fused), ("two-launch", call_two_launch)):
+        layers[0].kp.copy_(c.k_pool)
+        layers[0].vp.copy_(c.v_pool)
+        mk(0)()
+        torch.cuda.synchronize()
+        err = (outs[0][0].float().cpu() - want).abs().max().item()
+        pool_ok = torch.equal(layers[0].kp.cpu().view(torch.int16), kp0.view(torch.int16)) and \
+            torch.equal(layers[0].vp.cpu().view(torch.int16), vp0.view(torch.int16))
+        log(f"parity ({name}): max abs err {err:.2e}, append bit-exact {pool_ok}")
+        if err > 2e-3 or not pool_ok:
+            raise SystemExit(f"parity check failed ({name}: err {err}, append exact {pool_ok})")
 
     use_graph = not args.no_graph
-    us_call, steps = time_calls([call(i) for i in range(R)], args.steps, args.warmup, use_graph, args.repeats)
-    log(f"call (append + decode): {us_call:.2f} us")
-    us_eager, _ = time_calls([call(i) for i in range(R)], max(R, args.steps // 4), R, False, 3)
-    log(f"call, eager launches: {us_eager:.2f} us")
+    us_call, steps = time_calls([call_fused(i) for i in range(R)], args.steps, args.warmup, use_graph,
+                                args.repeats)
+    log(f"call, fused append + decode (1 launch): {us_call:.2f} us")
+    us_two, _ = time_calls([call_two_launch(i) for i in range(R)], args.steps, args.warmup, use_graph,
+                           args.repeats)
+    log(f"call, append + decode op (2 launches): {us_two:.2f} us")
+    us_eager, _ = time_calls([call_fused(i) for i in range(R)], max(R, args.steps // 4), R, False, 3)
+    log(f"call, fused, eager launches: {us_eager:.2f} us")
     us_dec, _ = time_calls([decode_only(i) for i in range(R)], args.steps, args.warmup, use_graph, args.repeats)
-    log(f"decode op alone: {us_dec:.2f} us")
+    log(f"decode op alone (1 launch): {us_dec:.2f} us")
 
     attended_list = case.attended.tolist()
     bytes_call = ref.decode_algorithmic_bytes(attended_list, 14, 2, 64, 16)
-    append_bytes = 2 * case.B * 2 * 64 * 2 * 2 + 16 * case.B
-    bytes_dec = bytes_call - append_bytes
     gbps = bytes_call / (us_call * 1e-6) / 1e9
-    dec_gbps = bytes_dec / (us_dec * 1e-6) / 1e9
+    us_ceil, ceil_bytes = gather_ceiling(dev, bytes_call, args.steps, args.warmup, args.repeats)
+    ceil_gbps = ceil_bytes / (us_ceil * 1e-6) / 1e9
+    log(f"paged-gather ceiling (probe, 2 KiB chunks): {us_ceil:.2f} us, {ceil_gbps:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -250,7 +294,7 @@ def main():
                          f"{threads} threads on {cpu_model()}"}
         log(f"cpu baseline: {cpu_us:.0f} us/call on {threads} threads")
 
-    wl = ("paged GQA decode call = KV append + split-KV load + merge, one layer" if args.config == 2
+    wl = ("paged GQA decode call = KV append + split-KV load + merge, one layer, one launch" if args.config == 2
           else "long-context paged GQA decode call (config 4)")
     line = {
         "metric": METRIC,
@@ -263,6 +307,8 @@ def main():
         "us_per_call": round(us_call, 3),
         "pct_of_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 1),
         "us_per_call_eager": round(us_eager, 3),
+        "us_per_call_two_launch": round(us_two, 3),
+        "us_decode_op_alone": round(us_dec, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -283,14 +329,20 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode op (paged_decode split + merge kernels)",
-            "achieved": round(dec_gbps, 1),
+            "kernel": "decode_kernel<64,4,append> (fused append + split-KV + merge, 1 launch/call)",
+            "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
-            "us_per_launch": round(us_dec, 3),
-            "algorithmic_bytes_per_launch": bytes_dec,
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "us_per_launch": round(us_call, 3),
+            "algorithmic_bytes_per_launch": bytes_call,
             "traffic": None,
+        },
+        "paged_gather_ceiling": {
+            "what": "probe kernel reading the call's byte volume as shuffled 2 KiB chunks (no math)",
+            "value": round(ceil_gbps, 1), "unit": "GB/s", "us": round(us_ceil, 3),
+            "frac_of_peak": round(ceil_gbps / HBM_PEAK_GBPS, 4),
+            "decode_frac_of_ceiling": round(gbps / ceil_gbps, 4),
         },
         "cpu_baseline": cpu,
     }

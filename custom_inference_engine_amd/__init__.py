@@ -11,7 +11,9 @@ from .attn.core import (  # noqa: F401
     GQA_PREFILL_CONFIG,
     HipQwen2Attention,
     TritonQwen2Attention,
+    decode_append_gqa_attention,
     decode_gqa_attention,
+    gqa_decode_append_attention_op,
     gqa_decode_attention_op,
     gqa_mixed_attention_op,
     mixed_gqa_attention,

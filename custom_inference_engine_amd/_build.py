@@ -19,7 +19,7 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libcie_paged.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ("capi.hip", "kv_append.hip", "paged_decode.hip", "mixed_attention.hip")
+SOURCES = ("capi.hip", "kv_append.hip", "paged_decode.hip", "mixed_attention.hip", "probe.hip")
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in device code.
@@ -45,15 +45,21 @@ def hipcc() -> str:
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
     cmd = [hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
-           os.path.join(CSRC, src), "-o", obj]
+           os.path.join(CSRC, src), "-o", obj, "-Rpass-analysis=kernel-resource-usage"]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature.
     noise = "is not a recognized feature for this target"
-    msg = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
+    lines = [l for l in (res.stdout + res.stderr).splitlines() if noise not in l]
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {src}:\n{msg}")
+        raise RuntimeError(f"hipcc failed on {src}:\n" + "\n".join(lines))
+    # Hot kernels must stay in registers: any scratch use is a build error.
+    spills = [l for l in lines if "ScratchSize [bytes/lane]:" in l and not l.rstrip().endswith(": 0")
+              and "ScratchSize [bytes/lane]: 0 " not in l]
+    if spills:
+        raise RuntimeError(f"{src}: kernel uses scratch memory (register spill):\n" + "\n".join(spills))
+    msg = "\n".join(l for l in lines if "remark:" not in l)
     if verbose and msg.strip():
         print(msg, flush=True)
     return obj

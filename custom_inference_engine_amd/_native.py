@@ -35,12 +35,19 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64p, _c_i64p,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
-    "cie_paged_decode_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "cie_paged_decode_partials_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "cie_paged_decode_max_splits": (ctypes.c_int, []),
     "cie_paged_decode": (
         ctypes.c_int,
-        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64p, _c_i64p, _c_i64p, _c_ptr, _c_i64, _c_i64,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64p, _c_i64p, _c_i64p, _c_ptr, _c_ptr, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_ptr, _c_ptr],
+    ),
+    "cie_paged_decode_append": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64p,
+         _c_i64p, _c_i64p, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
     "cie_mixed_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "cie_mixed_attention": (
@@ -49,9 +56,12 @@ _SIGNATURES = {
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
+    "cie_probe_gather_read": (
+        ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

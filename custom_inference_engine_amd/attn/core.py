@@ -15,20 +15,27 @@ Same surface as the reference's attn/core.py:
 The Triton launch knobs (``BLOCK_N``, ``BLOCK_M``, ``num_warps``, ``wrap``) are
 accepted and ignored.  Validation mirrors the reference's asserts and raises
 ``AssertionError`` with the same conditions (never stripped by ``-O``).
-Outputs and split workspaces are allocated with ``torch.empty`` on the
-current stream, so under graph capture they come from the graph pool.
+Outputs are allocated with ``torch.empty`` on the current stream (under graph
+capture they come from the graph pool), split partials likewise; the decode
+kernels' arrival counters are one persistent, self-cleaning buffer per device
+(``decode_counters``).
+The decode op also has a fused form, ``inference::gqa_decode_append_attention``,
+that performs ``KVStorage.decode_update`` and the decode in one launch.
 """
 from __future__ import annotations
+
+import threading
 
 import torch
 from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention, apply_rotary_pos_emb
 
 from .. import _native
 
-# Decode kernel geometry: waves per workgroup of the split kernel.
-DECODE_WAVES_PER_SPLIT = 4
-# Target resident wavefronts for the split grid (256 CUs x 16 waves).
-DECODE_TARGET_WAVES = 4096
+# Decode kernel geometry: one split = one workgroup of 8 wavefronts, which is
+# what one CU holds at the kernel's register use; the split count aims at one
+# workgroup per CU (MI355X: 256 CUs), i.e. one resident round.
+DECODE_WAVES_PER_SPLIT = 8
+DECODE_DEFAULT_CUS = 256
 DECODE_MAX_SPLITS = 64
 
 
@@ -49,10 +56,49 @@ def _block_table(bt: torch.Tensor) -> torch.Tensor:
     return bt
 
 
-def default_decode_splits(batch: int, h_kv: int) -> int:
-    """Split count that puts about DECODE_TARGET_WAVES waves on the chip."""
-    units = max(1, batch * h_kv * DECODE_WAVES_PER_SPLIT)
-    return max(1, min(DECODE_MAX_SPLITS, -(-DECODE_TARGET_WAVES // units)))
+_ctr_lock = threading.Lock()
+_ctr_cache: dict[int, torch.Tensor] = {}
+_ctr_retired: list[torch.Tensor] = []
+
+
+def decode_counters(dev: torch.device, n: int) -> torch.Tensor:
+    """The device's persistent split-arrival counters (zeroed once, kept zero by the kernel).
+
+    The decode kernel's counters must be zero before a call and are left zero
+    by it, so one buffer serves every stream-ordered call on a device, graph
+    replays included, without a clearing launch.  Calls that can overlap in
+    time (different streams) must pass their own zeroed ``counters``.
+    Replaced buffers stay alive: a captured graph may still point at them.
+    """
+    with _ctr_lock:
+        buf = _ctr_cache.get(dev.index)
+        if buf is None or buf.numel() < n:
+            if buf is not None:
+                _ctr_retired.append(buf)
+            buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=dev)
+            _ctr_cache[dev.index] = buf
+        return buf
+
+
+def _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters):
+    partials = torch.empty(lib.cie_paged_decode_partials_bytes(B, H_q, D, P), dtype=torch.uint8,
+                           device=dev)
+    if counters is None:
+        counters = decode_counters(dev, B * H_kv)
+    _require(counters.dtype == torch.int32 and counters.numel() >= B * H_kv, "counters too small")
+    return partials, counters
+
+
+def _cu_count(dev: torch.device | None) -> int:
+    if dev is not None and dev.type == "cuda":
+        return torch.cuda.get_device_properties(dev).multi_processor_count
+    return DECODE_DEFAULT_CUS
+
+
+def default_decode_splits(batch: int, h_kv: int, dev: torch.device | None = None) -> int:
+    """KV splits per (sequence, kv head): about one split workgroup per CU."""
+    units = max(1, batch * h_kv)
+    return max(1, min(DECODE_MAX_SPLITS, round(_cu_count(dev) / units)))
 
 
 def _check_pool(q, k, v):
@@ -66,7 +112,7 @@ def _check_pool(q, k, v):
 
 
 def decode_gqa_attention(q, k, v, lens, slot_ids, block_table, num_programs=None,
-                         BLOCK_N=64, num_warps=4, wrap=None, err=None):
+                         BLOCK_N=64, num_warps=4, wrap=None, err=None, counters=None):
     """Paged GQA decode: ``o[0, b, h] = softmax(q[0, b, h] K^T / sqrt(D)) V`` over ``lens[b]`` tokens.
 
     q: (1, B, H_q, D) fp16 contiguous; k, v: (n_pages, H_kv, page_size, D);
@@ -83,18 +129,20 @@ def decode_gqa_attention(q, k, v, lens, slot_ids, block_table, num_programs=None
     _check_pool(q, k, v)
     dev = _native.require_device(q, k, v, lens, slot_ids, block_table)
     lens, slot_ids, block_table = _index(lens), _index(slot_ids), _block_table(block_table)
-    P = int(num_programs) if num_programs else default_decode_splits(B, H_kv)
+    P = int(num_programs) if num_programs else default_decode_splits(B, H_kv, dev)
     _require(P >= 1, "num_programs must be >= 1")
 
     lib = _native.load()
     o = torch.empty_like(q)
     if B == 0:
         return o
-    ws = torch.empty(lib.cie_paged_decode_workspace_bytes(B, H_q, D, P), dtype=torch.uint8, device=dev)
+    _require(P <= lib.cie_paged_decode_max_splits(), "num_programs above the kernel's split limit")
+    partials, counters = _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters)
     _native.check(
         lib.cie_paged_decode(
             o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-            lens.data_ptr(), slot_ids.data_ptr(), block_table.data_ptr(), ws.data_ptr(),
+            lens.data_ptr(), slot_ids.data_ptr(), block_table.data_ptr(), partials.data_ptr(),
+            counters.data_ptr(),
             B, H_q, H_kv, D, PAGE_SIZE, N_PAGES, k.stride(0), k.stride(1),
             block_table.stride(0), block_table.shape[1], block_table.shape[0], P,
             _native.ptr(err), _native.stream_handle(dev),
@@ -102,6 +150,63 @@ def decode_gqa_attention(q, k, v, lens, slot_ids, block_table, num_programs=None
         "cie_paged_decode",
     )
     return o
+
+
+def decode_append_gqa_attention(q, k_cache, v_cache, k, v, lens, slot_ids, block_table,
+                                num_programs=None, err=None, counters=None):
+    """KV append of the new token + paged GQA decode in one launch.
+
+    Same result as ``KVStorage.decode_update`` (kv_cache/storage.py:87-122)
+    followed by ``decode_gqa_attention(..., lens[slot_ids] + 1, ...)``
+    (attn/core.py:200-215): the pools gain k[b] / v[b] at position
+    ``lens[slot_ids[b]]`` and each sequence attends that many tokens plus one.
+    ``lens`` is the pool's per-slot length (n_slots,), not advanced here.
+    """
+    total_T, H_q, D = q.shape[1:]
+    N_PAGES, H_kv, PAGE_SIZE, _ = k_cache.shape
+    B = slot_ids.shape[0]
+    _require(H_q % H_kv == 0, "H_q must be a multiple of H_kv")
+    _require(N_PAGES == block_table.shape[1], "block_table width must equal n_pages")
+    _require(total_T == B, "decode takes one query token per sequence")
+    _require(q.is_contiguous(), "q must be contiguous")
+    _check_pool(q, k_cache, v_cache)
+    dev = _native.require_device(q, k_cache, v_cache, k, v, lens, slot_ids, block_table)
+    kr, vr = _as_rows(k, H_kv, D), _as_rows(v, H_kv, D)
+    _require(kr.shape[0] == B and vr.shape[0] == B, "one new K/V row per sequence")
+    _require(kr.dtype == torch.float16 and vr.dtype == torch.float16, "new K/V must be float16")
+    lens, slot_ids, block_table = _index(lens), _index(slot_ids), _block_table(block_table)
+    P = int(num_programs) if num_programs else default_decode_splits(B, H_kv, dev)
+    _require(P >= 1, "num_programs must be >= 1")
+
+    lib = _native.load()
+    o = torch.empty_like(q)
+    if B == 0:
+        return o
+    _require(P <= lib.cie_paged_decode_max_splits(), "num_programs above the kernel's split limit")
+    partials, counters = _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters)
+    _native.check(
+        lib.cie_paged_decode_append(
+            o.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+            kr.data_ptr(), vr.data_ptr(), kr.stride(0), kr.stride(1), vr.stride(0), vr.stride(1),
+            lens.data_ptr(), slot_ids.data_ptr(), block_table.data_ptr(), partials.data_ptr(),
+            counters.data_ptr(),
+            B, H_q, H_kv, D, PAGE_SIZE, N_PAGES, k_cache.stride(0), k_cache.stride(1),
+            block_table.stride(0), block_table.shape[1], lens.shape[0], P,
+            _native.ptr(err), _native.stream_handle(dev),
+        ),
+        "cie_paged_decode_append",
+    )
+    return o
+
+
+def _as_rows(x: torch.Tensor, h_kv: int, d: int) -> torch.Tensor:
+    try:
+        rows = x.view(-1, h_kv, d)
+    except RuntimeError:
+        rows = x.reshape(-1, h_kv, d)
+    if rows.stride(2) != 1 or rows.stride(0) % 8 or rows.stride(1) % 8 or rows.data_ptr() % 16:
+        rows = rows.contiguous()
+    return rows
 
 
 def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids, block_table,
@@ -163,6 +268,20 @@ def _(q, k, v, lens, slot_ids, block_table):
     return torch.empty_like(q)
 
 
+@torch.library.custom_op("inference::gqa_decode_append_attention", mutates_args=("k_cache", "v_cache"))
+def gqa_decode_append_attention_op(
+    q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor,
+    v: torch.Tensor, lens: torch.Tensor, slot_ids: torch.Tensor, block_table: torch.Tensor,
+) -> torch.Tensor:
+    return decode_append_gqa_attention(q, k_cache, v_cache, k, v, lens, slot_ids, block_table,
+                                       **GQA_DECODE_CONFIG)
+
+
+@gqa_decode_append_attention_op.register_fake
+def _(q, k_cache, v_cache, k, v, lens, slot_ids, block_table):
+    return torch.empty_like(q)
+
+
 @torch.library.custom_op("inference::gqa_mixed_attention", mutates_args=())
 def gqa_mixed_attention_op(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -205,6 +324,9 @@ class TritonQwen2Attention(torch.nn.Module):
             self.register_buffer("qkv_weight", torch.cat([p.weight for p in projs]), persistent=False)
             self.register_buffer("qkv_bias", torch.cat([p.bias for p in projs]), persistent=False)
         self.fuse_qkv = True
+        # decode branch: KV append fused into the decode launch (one kernel)
+        # instead of decode_update + gqa_decode_attention (two).
+        self.fuse_append = True
 
     def forward(self, hidden_states, position_embeddings, attention_mask=None,
                 past_key_values=None, kv_manager=None, **kwargs):
@@ -230,7 +352,12 @@ class TritonQwen2Attention(torch.nn.Module):
         query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin,
                                                         unsqueeze_dim=2)
 
-        if metadata.full_decode:
+        if metadata.full_decode and self.fuse_append:
+            o = gqa_decode_append_attention_op(
+                query_states, kv_manager.keys[self.layer_idx], kv_manager.values[self.layer_idx],
+                key_states, value_states, kv_manager.lens, metadata.slot_ids, kv_manager.block_table,
+            )
+        elif metadata.full_decode:
             kv_manager.decode_update(self.layer_idx, metadata.slot_ids, key_states, value_states)
             o = gqa_decode_attention_op(
                 query_states, kv_manager.keys[self.layer_idx], kv_manager.values[self.layer_idx],

@@ -99,13 +99,15 @@ __device__ __forceinline__ void load_pair(KVPair<D>& kv, const f16* __restrict__
 }
 
 // Zero the V rows at keys >= key_end (the masked loads of the reference read
-// 0 there; pool memory past a sequence's end may hold anything).
+// 0 there; pool memory past a sequence's end may hold anything).  key0a /
+// key0b: first key of the pair's two tiles.
 template <int D>
-__device__ __forceinline__ void zero_tail_rows(KVPair<D>& kv, int key0, int key_end, int grp) {
+__device__ __forceinline__ void zero_tail_rows(KVPair<D>& kv, int key0a, int key0b, int key_end,
+                                               int grp) {
   typedef typename HVec<Geo<D>::NT>::type vrow_t;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int key = key0 + 16 * (e >> 2) + 4 * grp + (e & 3);
+    const int key = (e < 4 ? key0a : key0b) + 4 * grp + (e & 3);
     if (key >= key_end) kv.v[e] = vrow_t{};
   }
 }
@@ -128,13 +130,15 @@ struct SoftmaxAcc {
   }
 };
 
-// One 32-key step for NCT column tiles.  key0 = absolute index of the pair's
-// first key.  A column attends key j iff j < lim[c] (per lane: causal / length
-// limit of the lane's column).
+// One 32-key step for NCT column tiles.  key0a / key0b = absolute index of the
+// first key of the pair's two tiles (the tiles need not be adjacent; an absent
+// second tile passes a key0b past every limit).  A column attends key j iff
+// j < lim[c] (per lane: causal / length limit of the lane's column).
 template <int D, int NCT>
 __device__ __forceinline__ void attend_pair(SoftmaxAcc<D, NCT>& st, const KVPair<D>& kv,
-                                            const f16x8 (&qop)[NCT][Geo<D>::KS], int key0,
-                                            const int (&lim)[NCT], float scale_log2, int grp) {
+                                            const f16x8 (&qop)[NCT][Geo<D>::KS], int key0a,
+                                            int key0b, const int (&lim)[NCT], float scale_log2,
+                                            int grp) {
   constexpr int KS = Geo<D>::KS;
   constexpr int NT = Geo<D>::NT;
   f16x8 va[NT];
@@ -152,11 +156,12 @@ __device__ __forceinline__ void attend_pair(SoftmaxAcc<D, NCT>& st, const KVPair
       s1 = mfma16x16x32(kv.k[1][ks], qop[c][ks], s1);
     }
     float sc[8];
-    const int kb = key0 + 4 * grp;
+    const int kba = key0a + 4 * grp;
+    const int kbb = key0b + 4 * grp;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      sc[r] = (kb + r < lim[c]) ? s0[r] * scale_log2 : kNegInf;
-      sc[4 + r] = (kb + 16 + r < lim[c]) ? s1[r] * scale_log2 : kNegInf;
+      sc[r] = (kba + r < lim[c]) ? s0[r] * scale_log2 : kNegInf;
+      sc[4 + r] = (kbb + r < lim[c]) ? s1[r] * scale_log2 : kNegInf;
     }
     float mb = sc[0];
 #pragma unroll
@@ -217,6 +222,11 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
                                              int key_end, const PagedSrc& src, float scale_log2,
                                              int r16, int grp) {
   if (t_begin >= t_end) return;
+  // Keys past this wave's range belong to another wave (or do not exist):
+  // the zero-filled second tile of an odd-length range must score -inf.
+  int lim_w[NCT];
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) lim_w[c] = min(lim[c], t_end * 16);
   KVPair<D> cur, nxt;
   auto fetch = [&](KVPair<D>& kv, int t) {
     const bool two = t + 1 < t_end;
@@ -230,8 +240,8 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
   fetch(cur, t_begin);
   for (int t = t_begin; t < t_end; t += 2) {
     if (t + 2 < t_end) fetch(nxt, t + 2);
-    if ((t + 2) * 16 > key_end) zero_tail_rows<D>(cur, t * 16, key_end, grp);
-    attend_pair<D, NCT>(st, cur, qop, t * 16, lim, scale_log2, grp);
+    if ((t + 2) * 16 > key_end) zero_tail_rows<D>(cur, t * 16, t * 16 + 16, key_end, grp);
+    attend_pair<D, NCT>(st, cur, qop, t * 16, t * 16 + 16, lim_w, scale_log2, grp);
     cur = nxt;
   }
 }

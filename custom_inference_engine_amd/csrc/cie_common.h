@@ -46,7 +46,9 @@ __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
 }
 
 __device__ __forceinline__ void set_err(int32_t* err, int bit) {
+#ifndef CIE_DECODE_TRACE
   if (err) atomicOr(err, bit);
+#endif
 }
 
 // Uniform (wave-invariant) value hint: lets the compiler keep it in an SGPR.

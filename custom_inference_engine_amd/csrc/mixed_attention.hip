@@ -91,7 +91,11 @@ __device__ __forceinline__ TilePlan tile_plan(int qt, const SeqInfo& s, int G) {
   t.n_ctiles = (t.n_combos + 15) >> 4;
   t.key_end = s.c + t.row0 + t.rows;
   t.n_ktiles = (t.key_end + 15) >> 4;
-  t.keypar = t.n_ctiles == 1;
+  // Only a sequence's last tile may run key-parallel: the extra split
+  // workgroups and the merge address partials by (sequence, column), one
+  // short tile per sequence.  Full 16-row tiles with <= 16 columns (G = 1)
+  // run row-parallel on one wave.
+  t.keypar = t.n_ctiles == 1 && t.row0 + t.rows == s.L;
   const int n_pairs = (t.n_ktiles + 1) >> 1;
   t.n_act = t.keypar ? max(1, min(kMixedSplits, (n_pairs + kMinPairsPerSplit - 1) / kMinPairsPerSplit))
                      : 1;

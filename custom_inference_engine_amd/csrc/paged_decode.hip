@@ -1,66 +1,233 @@
-// Split-KV paged GQA decode for gfx950.
+// Split-KV paged GQA decode for gfx950: one launch per call.
 //
 // Semantics follow decode_gqa_attention (attn/core.py:13-66): for sequence b,
-// query head h (kv head g = h / G) attends the first lens[b] tokens of slot
-// slot_ids[b]:  o = softmax(q . K^T * D^-0.5) . V, o = 0 when lens[b] == 0
-// (the -inf guard of kernels/decode_attention.py:260-264).
+// query head h (kv head g = h / G) attends the first L tokens of slot
+// slot_ids[b]: o = softmax(q . K^T * D^-0.5) . V, o = 0 when L == 0 (the
+// -inf guard of kernels/decode_attention.py:260-264).
+//
+// Two entry modes share the kernel:
+//  * plain  (cie_paged_decode): L = lens[b], the pool is read-only — the
+//    reference's gqa_decode_attention op.
+//  * append (cie_paged_decode_append): pos = lens_pool[slot], L = pos + 1; the
+//    new token's K/V rows are written to (block_table[slot, pos / P], pos % P)
+//    exactly as KVStorage.decode_update (kv_cache/storage.py:87-122) does, and
+//    the wave that owns that tile reads them from k_new / v_new instead of the
+//    pool, so the append costs no extra launch and no extra round trip.
 //
 // Work split.  Grid (n_splits, H_kv, B), WAVES wavefronts per workgroup.  The
 // reference interleaves 16-row blocks over its P programs
 // (kernels/decode_attention.py:71-75); here the ceil(L/16) key tiles of a
-// (sequence, kv head) are cut into n_splits*WAVES contiguous, balanced runs, one
-// per wave, so each wave streams a contiguous range of block-table entries.
-// A wave keeps the G query heads of its kv head as MFMA columns (see
-// attn_engine.h), the waves of a workgroup fold their softmax states through
-// LDS, and the workgroup writes one partial (m, l, acc) per head for its
-// split.  decode_merge_kernel then combines the splits with log-sum-exp,
-// as kernels/decode_attention.py:243-264 does.
+// (sequence, kv head) are cut into n_splits * WAVES contiguous, balanced runs,
+// one per wave.  A wave keeps the G query heads of its kv head as MFMA columns
+// (attn_engine.h); the waves of a workgroup fold their softmax states through
+// LDS.  With one split the workgroup writes o directly.  Otherwise it writes a
+// partial (m, l, acc) per head, and the last workgroup of the (sequence, kv
+// head) to finish — found with a device-scope counter — merges the splits with
+// log-sum-exp as kernels/decode_attention.py:243-264 does, writes o and resets
+// the counter to zero for the next call.
 #include "attn_engine.h"
+
+// Build-time tuning (defaults are the shipped configuration):
+//   CIE_DECODE_WAVES  wavefronts per workgroup
+//   CIE_DECODE_PF     32-key steps whose loads are in flight ahead of the math
+//   CIE_DECODE_MERGE  how the splits meet: 2 = last-arriver with agent-scope
+//                     (sc1) partial stores / loads, 1 = last-arriver with
+//                     release / acquire fences, 3 = a second merge launch
+#ifndef CIE_DECODE_WAVES
+#define CIE_DECODE_WAVES 8
+#endif
+#ifndef CIE_DECODE_PF
+#define CIE_DECODE_PF 1
+#endif
+#ifndef CIE_DECODE_MERGE
+#define CIE_DECODE_MERGE 2
+#endif
 
 namespace cie {
 
 struct DecodeParams {
   f16* o;
   const f16* q;
-  const f16* k_pool;
-  const f16* v_pool;
-  const int64_t* lens;
+  f16* k_pool;
+  f16* v_pool;
+  const f16* k_new;  // append mode: (B, H_kv, D) rows with the strides below
+  const f16* v_new;
+  int64_t k_tok_stride, k_head_stride, v_tok_stride, v_head_stride;
+  const int64_t* lens;  // plain: (B,) attended; append: (n_slots,) prior per slot
   const int64_t* slot_ids;
   const int64_t* block_table;
   float* part_m;    // (B, H_q, S)
   float* part_l;    // (B, H_q, S)
   float* part_acc;  // (B, H_q, S, D)
+  int32_t* counters;  // (B * H_kv), zero between calls
   int64_t pool_page_stride, pool_head_stride, bt_stride, n_pages;
   int32_t bt_width, n_slots, B, H_q, H_kv, G, page_size, n_splits;
   float scale_log2;
   int32_t* err;
 };
 
-// Attended length of sequence b, clamped to what its block-table row can
-// address; an invalid slot attends nothing.
-__device__ __forceinline__ int decode_len(const DecodeParams& p, int b, int64_t& slot) {
+// Attended length of sequence b (clamped to what its block-table row can
+// address; an invalid slot attends nothing) and, in append mode, the new
+// token's position (-1 when there is nothing to append).
+template <bool kAppend>
+__device__ __forceinline__ int decode_len(const DecodeParams& p, int b, int64_t& slot, int& pos) {
+  pos = -1;
   slot = p.slot_ids[b];
   if (slot < 0 || slot >= p.n_slots) {
     set_err(p.err, CIE_ERRBIT_PAGE);
     slot = 0;
     return 0;
   }
-  int64_t L = p.lens[b];
   const int64_t cap = (int64_t)p.bt_width * p.page_size;
-  if (L < 0 || L > cap) {
-    set_err(p.err, CIE_ERRBIT_LEN);
-    L = L < 0 ? 0 : cap;
+  if constexpr (kAppend) {
+    const int64_t prior = p.lens[slot];
+    if (prior < 0 || prior + 1 > cap) {
+      set_err(p.err, CIE_ERRBIT_LEN);
+      return 0;
+    }
+    pos = (int)prior;
+    return pos + 1;
+  } else {
+    int64_t L = p.lens[b];
+    if (L < 0 || L > cap) {
+      set_err(p.err, CIE_ERRBIT_LEN);
+      L = L < 0 ? 0 : cap;
+    }
+    return (int)L;
   }
-  return (int)L;
 }
 
-template <int D, int WAVES>
-__global__ __launch_bounds__(WAVES * kWave) void decode_split_kernel(DecodeParams p) {
+// Append mode: point the lanes that hold key `pos` at the new rows instead of
+// the pool, and after the loads land, store those rows into the pool.
+template <int D>
+struct NewRow {
+  const f16* k;  // k_new row of (b, g)
+  const f16* v;  // v_new row of (b, g)
+  int pos;       // absolute key index of the new token (-1: none)
+};
+
+// Loads of one 16-key tile; the lanes holding key nr.pos read the new rows.
+template <int D>
+__device__ __forceinline__ void load_tile_new(f16x8 (&k)[Geo<D>::KS],
+                                              typename HVec<Geo<D>::NT>::type (&v)[4],
+                                              const PagedSrc& src, TileLoc tl, int kt0,
+                                              const NewRow<D>& nr, int r16, int grp) {
+  constexpr int KS = Geo<D>::KS;
+  constexpr int NT = Geo<D>::NT;
+  typedef typename HVec<NT>::type vrow_t;
+  const f16* kp = (kt0 + r16 == nr.pos) ? nr.k + 8 * grp : src.k_pool + tl.base + r16 * D + 8 * grp;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) k[ks] = *reinterpret_cast<const f16x8*>(kp + 32 * ks);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int row = 4 * grp + e;
+    const f16* vp = (kt0 + row == nr.pos) ? nr.v + NT * r16 : src.v_pool + tl.base + row * D + NT * r16;
+    v[e] = *reinterpret_cast<const vrow_t*>(vp);
+  }
+}
+
+template <int D, bool kAppend>
+__device__ __forceinline__ void load_pair_new(KVPair<D>& kv, const PagedSrc& src, TileLoc t0,
+                                              TileLoc t1, bool two, int key0a, int key0b,
+                                              const NewRow<D>& nr, int r16, int grp) {
+  typedef typename HVec<Geo<D>::NT>::type vrow_t;
+  typedef vrow_t vquad_t[4];
+  if constexpr (!kAppend) {
+    load_pair<D>(kv, src.k_pool, src.v_pool, t0, t1, two, r16, grp);
+  } else {
+    load_tile_new<D>(kv.k[0], *reinterpret_cast<vquad_t*>(&kv.v[0]), src, t0, key0a, nr, r16, grp);
+    if (two) {
+      load_tile_new<D>(kv.k[1], *reinterpret_cast<vquad_t*>(&kv.v[4]), src, t1, key0b, nr, r16,
+                       grp);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < Geo<D>::KS; ++ks) kv.k[1][ks] = f16x8{};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kv.v[4 + e] = vrow_t{};
+    }
+  }
+}
+
+// Store the new token's rows (already in registers) into the pool.  The
+// register arrays are only ever indexed with compile-time indices (a runtime
+// index would move the whole pair to scratch memory).
+template <int D>
+__device__ __forceinline__ void store_new_row(const KVPair<D>& kv, const PagedSrc& src,
+                                              TileLoc t0, TileLoc t1, int key0a, int key0b,
+                                              int pos, int r16, int grp) {
+  constexpr int KS = Geo<D>::KS;
+  constexpr int NT = Geo<D>::NT;
+  typedef typename HVec<NT>::type vrow_t;
+  const bool second = pos >= key0b;
+  const int row = pos - (second ? key0b : key0a);
+  const int64_t base = (second ? t1.base : t0.base) + (int64_t)row * D;
+  f16* kpool = const_cast<f16*>(src.k_pool);
+  f16* vpool = const_cast<f16*>(src.v_pool);
+  if (r16 == row) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const f16x8 kk = second ? kv.k[1][ks] : kv.k[0][ks];
+      *reinterpret_cast<f16x8*>(kpool + base + 8 * grp + 32 * ks) = kk;
+    }
+  }
+  if ((row >> 2) == grp) {
+    vrow_t vv = vrow_t{};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e == 4 * (int)second + (row & 3)) vv = kv.v[e];
+    *reinterpret_cast<vrow_t*>(vpool + base + NT * r16) = vv;
+  }
+}
+
+// Split partials cross workgroups (and XCDs, each with its own L2).  With the
+// fence-free merge they are written and read as agent-scope atomics
+// (global_store / global_load ... sc1), coherent device-wide.
+__device__ __forceinline__ void partial_store(float* ptr, float v) {
+#if CIE_DECODE_MERGE == 2
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  *ptr = v;
+#endif
+}
+__device__ __forceinline__ float partial_load(const float* ptr) {
+#if CIE_DECODE_MERGE == 2
+  return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#else
+  return *ptr;
+#endif
+}
+
+constexpr int kMaxSplits = 64;  // LDS staging bound of the merge (G <= 16)
+
+template <int D, int NTHREADS>
+__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g, float* sm_ms,
+                                             float* sm_ls);
+
+// Profiling builds only (-DCIE_DECODE_TRACE): wave 0 of every workgroup
+// stamps phase boundaries (s_memrealtime) into the buffer passed as `err`.
+#ifdef CIE_DECODE_TRACE
+#define DECODE_TRACE(k, v)                                                                \
+  do {                                                                                    \
+    if (threadIdx.x == 0 && p.err != nullptr) {                                         \
+      __builtin_amdgcn_s_waitcnt(0);                                                      \
+      reinterpret_cast<uint64_t*>(p.err)[((int64_t)(b * p.H_kv + g) * p.n_splits + split) * 8 + \
+                                         (k)] = (v);                                      \
+    }                                                                                     \
+  } while (0)
+#else
+#define DECODE_TRACE(k, v) \
+  do {                     \
+  } while (0)
+#endif
+
+template <int D, int WAVES, bool kAppend>
+__global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   constexpr int KS = Geo<D>::KS;
   constexpr int NT = Geo<D>::NT;
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
   __shared__ float sm_acc[WAVES][16][D + 1];
+  __shared__ int sm_last;
 
   const int split = blockIdx.x;
   const int g = blockIdx.y;
@@ -69,14 +236,65 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_split_kernel(DecodeParam
   const int wave = threadIdx.x / kWave;
   const int r16 = lane & 15;
   const int grp = lane >> 4;
+  const int S = p.n_splits;
 
-  int64_t slot;
-  const int L = decode_len(p, b, slot);
-  const int n_tiles = (L + 15) >> 4;
-  const int total_waves = p.n_splits * WAVES;
+  DECODE_TRACE(0, __builtin_amdgcn_s_memrealtime());
+  DECODE_TRACE(5, (uint64_t)__builtin_amdgcn_s_getreg(0xF804));  // HW_ID
+  DECODE_TRACE(6, (uint64_t)__builtin_amdgcn_s_getreg(0xF814));  // XCC_ID
+
+  // Wave gw of the TW waves of this (sequence, kv head) takes key tiles
+  // gw, gw + TW, gw + 2*TW, ...  Its k-th tile's page id is held by lane k
+  // (read back with readlane), so a step never waits on a block-table load,
+  // and the first kSpecTiles ids are fetched as soon as the slot is known —
+  // in parallel with the length, which in append mode is itself a load
+  // indexed by the slot.
+  const int TW = S * WAVES;
   const int gw = split * WAVES + wave;
-  const int t_begin = (int)((int64_t)n_tiles * gw / total_waves);
-  const int t_end = (int)((int64_t)n_tiles * (gw + 1) / total_waves);
+  int64_t slot = p.slot_ids[b];
+  const bool slot_ok = slot >= 0 && slot < p.n_slots;
+  if (!slot_ok) {
+    set_err(p.err, CIE_ERRBIT_PAGE);
+    slot = 0;
+  }
+  const int64_t* bt_row = p.block_table + slot * p.bt_stride;
+  const int tpp = p.page_size >> 4;  // 16-key tiles per page
+  const int row_tiles = p.bt_width * tpp;
+  auto lane_page = [&](int k) -> int {  // page id of this wave's k-th tile
+    const int t = gw + k * TW;
+    if (t >= row_tiles) return 0;
+    int64_t page = bt_row[t / tpp];
+    if (page < 0 || page >= p.n_pages) {
+      set_err(p.err, CIE_ERRBIT_PAGE);
+      page = 0;
+    }
+    return (int)page;
+  };
+  constexpr int kSpecTiles = 16;
+  int pages = lane < kSpecTiles ? lane_page(lane) : 0;
+
+  int L, pos = -1;
+  {
+    const int64_t cap = (int64_t)row_tiles * 16;
+    if constexpr (kAppend) {
+      const int64_t prior = p.lens[slot];
+      if (!slot_ok || prior < 0 || prior + 1 > cap) {
+        if (slot_ok) set_err(p.err, CIE_ERRBIT_LEN);
+        L = 0;
+      } else {
+        pos = (int)prior;
+        L = pos + 1;
+      }
+    } else {
+      int64_t len = p.lens[b];
+      if (len < 0 || len > cap) {
+        set_err(p.err, CIE_ERRBIT_LEN);
+        len = len < 0 ? 0 : cap;
+      }
+      L = slot_ok ? (int)len : 0;
+    }
+  }
+  const int n_tiles = (L + 15) >> 4;
+  const int n_mine = n_tiles > gw ? (n_tiles - gw + TW - 1) / TW : 0;
 
   // Q^T operand: column r16 = head g*G + r16 (zero past the group).
   f16x8 qop[1][KS];
@@ -84,16 +302,79 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_split_kernel(DecodeParam
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
     qop[0][ks] = (r16 < p.G) ? *reinterpret_cast<const f16x8*>(qrow + 32 * ks) : f16x8{};
-  const int lim[1] = {L};
 
+  const PagedSrc src{p.k_pool,  p.v_pool,  bt_row, (int64_t)g * p.pool_head_stride,
+                     p.pool_page_stride, p.n_pages, p.page_size, p.err};
+  NewRow<D> nr{nullptr, nullptr, -1};
+  if constexpr (kAppend) {
+    nr.k = p.k_new + (int64_t)b * p.k_tok_stride + (int64_t)g * p.k_head_stride;
+    nr.v = p.v_new + (int64_t)b * p.v_tok_stride + (int64_t)g * p.v_head_stride;
+    nr.pos = pos;
+  }
+
+  DECODE_TRACE(1, __builtin_amdgcn_s_memrealtime());
+  DECODE_TRACE(7, (uint64_t)n_mine);
   SoftmaxAcc<D, 1> st;
   st.init();
+  const int lim[1] = {L};
+  constexpr int kNoKey = 0x3fffffff;  // key base of an absent second tile: masked everywhere
+  for (int c0 = 0; c0 < n_mine; c0 += kWave) {
+    // this chunk's page ids: lanes k = c0 + lane (the first chunk's first
+    // kSpecTiles are already in flight)
+    if (c0 > 0 || n_mine > kSpecTiles) {
+      const int k = c0 + lane;
+      if (c0 > 0 || lane >= kSpecTiles) pages = k < n_mine ? lane_page(k) : 0;
+    }
+    const int n_chunk = min(kWave, n_mine - c0);
+    const int n_pairs = (n_chunk + 1) >> 1;
+    // Ring of kPF + 1 register-staged pairs: pair j's loads are issued kPF
+    // steps before its math, so up to kPF pairs of loads are in flight.
+    constexpr int kPF = CIE_DECODE_PF;
+    KVPair<D> ring[kPF + 1];
+    TileLoc loc[kPF + 1][2];
+    int keya[kPF + 1], keyb[kPF + 1];
+    auto issue = [&](int slot_i, int j) {
+      const int ka = 2 * j;                // chunk-local index of tile A
+      const bool two = ka + 1 < n_chunk;
+      const int ta = gw + (c0 + ka) * TW;  // tile ids
+      const int tb = ta + TW;
+      const int pa = __builtin_amdgcn_readlane(pages, ka);
+      const int pb = two ? __builtin_amdgcn_readlane(pages, ka + 1) : pa;
+      loc[slot_i][0] = TileLoc{(int64_t)pa * src.page_stride + src.head_off +
+                               (int64_t)((ta % tpp) * 16) * D};
+      loc[slot_i][1] = TileLoc{(int64_t)pb * src.page_stride + src.head_off +
+                               (int64_t)((tb % tpp) * 16) * D};
+      keya[slot_i] = ta * 16;
+      keyb[slot_i] = two ? tb * 16 : kNoKey;
+      load_pair_new<D, kAppend>(ring[slot_i], src, loc[slot_i][0], loc[slot_i][1], two,
+                                keya[slot_i], keyb[slot_i], nr, r16, grp);
+    };
+#pragma unroll
+    for (int j = 0; j < kPF; ++j)
+      if (j < n_pairs) issue(j, j);
+    for (int j0 = 0; j0 < n_pairs; j0 += kPF + 1) {
+#pragma unroll
+      for (int u = 0; u <= kPF; ++u) {
+        const int j = j0 + u;
+        if (j < n_pairs) {
+          if (j + kPF < n_pairs) issue((u + kPF) % (kPF + 1), j + kPF);
+          KVPair<D>& cur = ring[u];
+          const int ka = keya[u], kb = keyb[u];
+          const int last_key = (kb == kNoKey ? ka : kb) + 16;
+          if (last_key >= L) {  // this pair holds the sequence's last key
+            zero_tail_rows<D>(cur, ka, kb, L, grp);
+            if constexpr (kAppend) {
+              // the new token is the sequence's last key: it sits in this pair
+              if (pos >= ka) store_new_row<D>(cur, src, loc[u][0], loc[u][1], ka, kb, pos, r16, grp);
+            }
+          }
+          attend_pair<D, 1>(st, cur, qop, ka, kb, lim, p.scale_log2, grp);
+        }
+      }
+    }
+  }
 
-  const PagedSrc src{p.k_pool,  p.v_pool,  p.block_table + slot * p.bt_stride,
-                     (int64_t)g * p.pool_head_stride, p.pool_page_stride, p.n_pages,
-                     p.page_size, p.err};
-  stream_tiles<D, 1>(st, qop, lim, t_begin, t_end, L, src, p.scale_log2, r16, grp);
-
+  DECODE_TRACE(2, __builtin_amdgcn_s_memrealtime());
   // Fold the waves of this workgroup.
   st.l[0] = col_sum4(st.l[0]);
   if (grp == 0) {
@@ -106,7 +387,6 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_split_kernel(DecodeParam
     for (int r = 0; r < 4; ++r) sm_acc[wave][r16][acc_dim<D>(grp, r, nt)] = st.acc[0][nt][r];
   __syncthreads();
 
-  const int S = p.n_splits;
   for (int it = threadIdx.x; it < p.G * D; it += WAVES * kWave) {
     const int h = it / D;
     const int d = it - h * D;
@@ -123,98 +403,158 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_split_kernel(DecodeParam
         den += a * sm_l[w][h];
       }
     }
-    const int64_t row = ((int64_t)b * p.H_q + g * p.G + h) * S + split;
-    p.part_acc[row * D + d] = num;
-    if (d == 0) {
-      p.part_m[row] = M;
-      p.part_l[row] = den;
-    }
-  }
-}
-
-// One wavefront per (query head, sequence): log-sum-exp merge of the splits.
-template <int D>
-__global__ __launch_bounds__(kWave) void decode_merge_kernel(DecodeParams p) {
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const int S = p.n_splits;
-  const int64_t row0 = ((int64_t)b * p.H_q + h) * S;
-  float M = kNegInf;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, p.part_m[row0 + s]);
-  for (int d = threadIdx.x; d < D; d += kWave) {
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const float ms = p.part_m[row0 + s];
-      if (ms != kNegInf) {
-        const float a = fast_exp2(ms - M);
-        num += a * p.part_acc[(row0 + s) * D + d];
-        den += a * p.part_l[row0 + s];
+    if (S == 1) {
+      p.o[((int64_t)b * p.H_q + g * p.G + h) * D + d] =
+          (f16)((M == kNegInf || den == 0.f) ? 0.f : num / den);
+    } else {
+      const int64_t row = ((int64_t)b * p.H_q + g * p.G + h) * S + split;
+      partial_store(&p.part_acc[row * D + d], num);
+      if (d == 0) {
+        partial_store(&p.part_m[row], M);
+        partial_store(&p.part_l[row], den);
       }
     }
-    const float out = (M == kNegInf) ? 0.f : num / den;
-    p.o[((int64_t)b * p.H_q + h) * D + d] = (f16)out;
+  }
+  DECODE_TRACE(3, __builtin_amdgcn_s_memrealtime());
+  if (S == 1) return;
+
+#if CIE_DECODE_MERGE != 3
+  // Last workgroup of this (sequence, kv head) to arrive merges the splits.
+#if CIE_DECODE_MERGE == 2
+  // Partials went out as agent-scope (sc1) stores; once they have completed
+  // (vmcnt 0) they are visible device-wide, so no L2 writeback is needed
+  // before the arrival count.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // s_waitcnt vmcnt(0)
+  __syncthreads();
+  if (threadIdx.x == 0)
+    sm_last = __hip_atomic_fetch_add(&p.counters[b * p.H_kv + g], 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+  __syncthreads();
+  if (!sm_last) return;
+#else
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    sm_last = __hip_atomic_fetch_add(&p.counters[b * p.H_kv + g], 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+  }
+  __syncthreads();
+  if (!sm_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#endif
+  // the fold's LDS is free again: reuse it to stage the splits' m / l
+  merge_splits<D, WAVES * kWave>(p, b, g, &sm_acc[0][0][0], &sm_acc[0][0][0] + 16 * kMaxSplits);
+  if (threadIdx.x == 0) p.counters[b * p.H_kv + g] = 0;
+  DECODE_TRACE(4, __builtin_amdgcn_s_memrealtime());
+#endif
+}
+
+// Combine the S partial states of every head of (b, g) into o.  The m / l of
+// all splits are staged in LDS first (scratch of >= G * S floats each).
+template <int D, int NTHREADS>
+__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g, float* sm_ms,
+                                             float* sm_ls) {
+  const int S = p.n_splits;
+  const int64_t row0 = ((int64_t)b * p.H_q + g * p.G) * S;
+  __syncthreads();
+  for (int i = threadIdx.x; i < p.G * S; i += NTHREADS) {
+    sm_ms[i] = partial_load(&p.part_m[row0 + i]);
+    sm_ls[i] = partial_load(&p.part_l[row0 + i]);
+  }
+  __syncthreads();
+  for (int it = threadIdx.x; it < p.G * D; it += NTHREADS) {
+    const int h = it / D;
+    const int d = it - h * D;
+    float M = kNegInf;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, sm_ms[h * S + s]);
+    float num = 0.f, den = 0.f;
+#pragma unroll 8
+    for (int s = 0; s < S; ++s) {
+      const float ms = sm_ms[h * S + s];
+      const float a = ms == kNegInf ? 0.f : fast_exp2(ms - M);
+      num += a * partial_load(&p.part_acc[(row0 + h * S + s) * D + d]);
+      den += a * sm_ls[h * S + s];
+    }
+    p.o[((int64_t)b * p.H_q + g * p.G + h) * D + d] =
+        (f16)((M == kNegInf || den == 0.f) ? 0.f : num / den);
   }
 }
 
-constexpr int kDecodeWaves = 4;
-
+// Separate merge launch (CIE_DECODE_MERGE == 3): one workgroup per (g, b).
 template <int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
+  __shared__ float sm_ms[16 * kMaxSplits];
+  __shared__ float sm_ls[16 * kMaxSplits];
+  merge_splits<D, 256>(p, blockIdx.y, blockIdx.x, sm_ms, sm_ls);
+}
+
+// Waves per workgroup: D = 128 needs twice the registers, so half the waves.
+template <int D>
+constexpr int decode_waves() {
+  return D <= 64 ? CIE_DECODE_WAVES : (CIE_DECODE_WAVES > 4 ? 4 : CIE_DECODE_WAVES);
+}
+
+template <int D, bool kAppend>
 static int launch_decode(const DecodeParams& p, hipStream_t stream) {
+  constexpr int W = decode_waves<D>();
   dim3 grid(p.n_splits, p.H_kv, p.B);
-  hipLaunchKernelGGL((decode_split_kernel<D, kDecodeWaves>), grid, dim3(kDecodeWaves * kWave),
-                     0, stream, p);
+  hipLaunchKernelGGL((decode_kernel<D, W, kAppend>), grid, dim3(W * kWave), 0, stream, p);
   int rc = (int)hipGetLastError();
-  if (rc) return rc;
-  hipLaunchKernelGGL((decode_merge_kernel<D>), dim3(p.H_q, p.B), dim3(kWave), 0, stream, p);
-  return (int)hipGetLastError();
+#if CIE_DECODE_MERGE == 3
+  if (rc == 0 && p.n_splits > 1) {
+    hipLaunchKernelGGL((decode_merge_kernel<D>), dim3(p.H_kv, p.B), dim3(256), 0, stream, p);
+    rc = (int)hipGetLastError();
+  }
+#endif
+  return rc;
 }
 
-}  // namespace cie
+// Partials buffer: part_m | part_l | part_acc (fp32), each region 256-byte aligned.
+struct PartLayout {
+  int64_t m, l, acc, total;
+};
 
-using namespace cie;
-
-extern "C" int64_t cie_paged_decode_workspace_bytes(int64_t B, int64_t H_q, int64_t D,
-                                                    int64_t n_splits) {
-  if (B < 0 || H_q <= 0 || D <= 0 || n_splits <= 0) return -1;
-  return B * H_q * n_splits * (D + 2) * (int64_t)sizeof(float);
+static PartLayout part_layout(int64_t B, int64_t H_q, int64_t D, int64_t S) {
+  auto up = [](int64_t x) { return (x + 255) & ~int64_t(255); };
+  const int64_t rows = B * H_q * S;
+  PartLayout w;
+  w.m = 0;
+  w.l = up(rows * 4);
+  w.acc = up(w.l + rows * 4);
+  w.total = up(w.acc + rows * D * 4);
+  return w;
 }
 
-extern "C" int cie_paged_decode(void* o, const void* q, const void* k_pool, const void* v_pool,
-                                const int64_t* lens, const int64_t* slot_ids,
-                                const int64_t* block_table, void* workspace, int64_t B,
-                                int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size,
-                                int64_t n_pages, int64_t pool_page_stride,
-                                int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
-                                int64_t n_slots, int64_t n_splits, int32_t* err, void* stream) {
+template <bool kAppend>
+static int decode_entry(DecodeParams& p, void* partials, int32_t* counters, int64_t B,
+                        int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size, int64_t n_pages,
+                        int64_t pool_page_stride, int64_t pool_head_stride, int64_t bt_stride,
+                        int64_t bt_width, int64_t n_slots, int64_t n_splits, int32_t* err,
+                        void* stream) {
   if (B < 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || n_pages <= 0 || bt_width <= 0 ||
       bt_stride < bt_width || n_slots <= 0 || n_splits <= 0 || page_size <= 0)
     return CIE_EINVAL;
   if (B == 0) return CIE_OK;
-  if (!o || !q || !k_pool || !v_pool || !lens || !slot_ids || !block_table || !workspace)
+  if (!p.o || !p.q || !p.k_pool || !p.v_pool || !p.lens || !p.slot_ids || !p.block_table)
     return CIE_EINVAL;
+  if (n_splits > 1 && (!partials || !counters)) return CIE_EINVAL;
   const int64_t G = H_q / H_kv;
-  if (G > 16 || page_size % 16 != 0 || B > 65535 || H_kv > 65535 || n_splits > 65535 ||
+  if (G > 16 || page_size % 16 != 0 || B > 65535 || H_kv > 65535 || n_splits > kMaxSplits ||
       bt_width * page_size > 0x7fffffff)
     return CIE_EUNSUPPORTED;
   if (D != 64 && D != 128) return CIE_EUNSUPPORTED;
-  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_pool) |
-       reinterpret_cast<uintptr_t>(v_pool)) & 15)
+  if ((reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k_pool) |
+       reinterpret_cast<uintptr_t>(p.v_pool) | reinterpret_cast<uintptr_t>(partials) |
+       reinterpret_cast<uintptr_t>(counters)) & 15)
     return CIE_EINVAL;
   if (pool_page_stride % 8 != 0 || pool_head_stride % 8 != 0) return CIE_EINVAL;
 
-  DecodeParams p{};
-  p.o = static_cast<f16*>(o);
-  p.q = static_cast<const f16*>(q);
-  p.k_pool = static_cast<const f16*>(k_pool);
-  p.v_pool = static_cast<const f16*>(v_pool);
-  p.lens = lens;
-  p.slot_ids = slot_ids;
-  p.block_table = block_table;
-  float* ws = static_cast<float*>(workspace);
-  const int64_t rows = B * H_q * n_splits;
-  p.part_m = ws;
-  p.part_l = ws + rows;
-  p.part_acc = ws + 2 * rows;
+  const PartLayout w = part_layout(B, H_q, D, n_splits);
+  char* ws = static_cast<char*>(partials);
+  p.part_m = reinterpret_cast<float*>(ws + w.m);
+  p.part_l = reinterpret_cast<float*>(ws + w.l);
+  p.part_acc = reinterpret_cast<float*>(ws + w.acc);
+  p.counters = counters;
   p.pool_page_stride = pool_page_stride;
   p.pool_head_stride = pool_head_stride;
   p.bt_stride = bt_stride;
@@ -230,5 +570,68 @@ extern "C" int cie_paged_decode(void* o, const void* q, const void* k_pool, cons
   p.scale_log2 = kLog2e / __builtin_sqrtf((float)D);
   p.err = err;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return D == 64 ? launch_decode<64>(p, s) : launch_decode<128>(p, s);
+  return D == 64 ? launch_decode<64, kAppend>(p, s) : launch_decode<128, kAppend>(p, s);
+}
+
+}  // namespace cie
+
+using namespace cie;
+
+extern "C" int64_t cie_paged_decode_partials_bytes(int64_t B, int64_t H_q, int64_t D,
+                                                   int64_t n_splits) {
+  if (B < 0 || H_q <= 0 || D <= 0 || n_splits <= 0) return -1;
+  return part_layout(B, H_q, D, n_splits).total;
+}
+
+extern "C" int cie_paged_decode_max_splits(void) { return kMaxSplits; }
+
+extern "C" int cie_paged_decode(void* o, const void* q, const void* k_pool, const void* v_pool,
+                                const int64_t* lens, const int64_t* slot_ids,
+                                const int64_t* block_table, void* partials, int32_t* counters,
+                                int64_t B, int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size,
+                                int64_t n_pages, int64_t pool_page_stride,
+                                int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
+                                int64_t n_slots, int64_t n_splits, int32_t* err, void* stream) {
+  DecodeParams p{};
+  p.o = static_cast<f16*>(o);
+  p.q = static_cast<const f16*>(q);
+  p.k_pool = const_cast<f16*>(static_cast<const f16*>(k_pool));
+  p.v_pool = const_cast<f16*>(static_cast<const f16*>(v_pool));
+  p.lens = lens;
+  p.slot_ids = slot_ids;
+  p.block_table = block_table;
+  return decode_entry<false>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages, pool_page_stride,
+                             pool_head_stride, bt_stride, bt_width, n_slots, n_splits, err,
+                             stream);
+}
+
+extern "C" int cie_paged_decode_append(
+    void* o, const void* q, void* k_pool, void* v_pool, const void* k_new, const void* v_new,
+    int64_t k_tok_stride, int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+    const int64_t* lens, const int64_t* slot_ids, const int64_t* block_table, void* partials,
+    int32_t* counters, int64_t B, int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size, int64_t n_pages,
+    int64_t pool_page_stride, int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
+    int64_t n_slots, int64_t n_splits, int32_t* err, void* stream) {
+  if (B > 0 && (!k_new || !v_new)) return CIE_EINVAL;
+  if (((reinterpret_cast<uintptr_t>(k_new) | reinterpret_cast<uintptr_t>(v_new)) & 15) ||
+      k_tok_stride % 8 != 0 || k_head_stride % 8 != 0 || v_tok_stride % 8 != 0 ||
+      v_head_stride % 8 != 0)
+    return CIE_EINVAL;
+  DecodeParams p{};
+  p.o = static_cast<f16*>(o);
+  p.q = static_cast<const f16*>(q);
+  p.k_pool = static_cast<f16*>(k_pool);
+  p.v_pool = static_cast<f16*>(v_pool);
+  p.k_new = static_cast<const f16*>(k_new);
+  p.v_new = static_cast<const f16*>(v_new);
+  p.k_tok_stride = k_tok_stride;
+  p.k_head_stride = k_head_stride;
+  p.v_tok_stride = v_tok_stride;
+  p.v_head_stride = v_head_stride;
+  p.lens = lens;
+  p.slot_ids = slot_ids;
+  p.block_table = block_table;
+  return decode_entry<true>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages, pool_page_stride,
+                            pool_head_stride, bt_stride, bt_width, n_slots, n_splits, err,
+                            stream);
 }

@@ -85,28 +85,62 @@ int cie_kv_append_tokens(void* k_pool, void* v_pool,
  * Split-KV paged GQA decode, one query token per sequence:
  *   o[b, h, :] = softmax(q[b, h, :] . K_b^T * D^-0.5) . V_b
  * over the first lens[b] tokens of slot slot_ids[b]'s pages, kv head h / G.
- * lens[b] == 0 gives o = 0.
+ * lens[b] == 0 gives o = 0.  One kernel launch: the KV splits, and the
+ * log-sum-exp merge done by the last workgroup of each (sequence, kv head).
  * Replaces decode_gqa_attention (attn/core.py:13-66), i.e. the Triton
  * decode_gqa_attention_kernel_load (kernels/decode_attention.py:12-179) and
  * decode_attention_kernel_merge (kernels/decode_attention.py:182-272).
  *   q, o       : (B, H_q, D) dense fp16
- *   workspace  : cie_paged_decode_workspace_bytes(B, H_q, D, n_splits) bytes,
- *                any contents (partial softmax state of the splits)
+ *   lens       : (B,) attended lengths (the reference passes lens[slot] + 1)
  *   n_splits   : KV splits per (sequence, kv head) — the reference's
- *                `num_programs`.
+ *                `num_programs`
+ *                (1 <= n_splits <= cie_paged_decode_max_splits())
+ *   partials   : cie_paged_decode_partials_bytes(B, H_q, D, n_splits) bytes,
+ *                16-byte aligned, any contents: the splits' softmax state
+ *   counters   : B * H_kv int32, 16-byte aligned: one arrival counter per
+ *                (sequence, kv head).  They must be zero before the call and
+ *                every completed call leaves them zero, so one zeroed buffer
+ *                serves any number of stream-ordered calls.  Calls that can
+ *                overlap in time must not share counters or partials.
+ *   partials and counters may be NULL when n_splits == 1.
  */
-int64_t cie_paged_decode_workspace_bytes(int64_t B, int64_t H_q, int64_t D,
-                                         int64_t n_splits);
+int64_t cie_paged_decode_partials_bytes(int64_t B, int64_t H_q, int64_t D,
+                                        int64_t n_splits);
+int cie_paged_decode_max_splits(void);
 int cie_paged_decode(void* o, const void* q,
                      const void* k_pool, const void* v_pool,
                      const int64_t* lens, const int64_t* slot_ids,
                      const int64_t* block_table,
-                     void* workspace,
+                     void* partials, int32_t* counters,
                      int64_t B, int64_t H_q, int64_t H_kv, int64_t D,
                      int64_t page_size, int64_t n_pages,
                      int64_t pool_page_stride, int64_t pool_head_stride,
                      int64_t bt_stride, int64_t bt_width, int64_t n_slots,
                      int64_t n_splits, int32_t* err, void* stream);
+
+/*
+ * Decode step with the KV append fused in, one launch: for each sequence b,
+ * pos = lens[slot_ids[b]] (the pool's prior length per slot, (n_slots,)),
+ * the new K/V rows k_new[b] / v_new[b] are written to
+ * (block_table[slot, pos / page_size], pos % page_size) bit-exactly, and o is
+ * the decode attention over the pos + 1 tokens that then exist.
+ * Equivalent to KVStorage.decode_update (kv_cache/storage.py:87-122) followed
+ * by gqa_decode_attention with lens[slot] + 1 (attn/core.py:200-215).
+ * partials / counters as for cie_paged_decode.
+ */
+int cie_paged_decode_append(void* o, const void* q, void* k_pool, void* v_pool,
+                            const void* k_new, const void* v_new,
+                            int64_t k_tok_stride, int64_t k_head_stride,
+                            int64_t v_tok_stride, int64_t v_head_stride,
+                            const int64_t* lens, const int64_t* slot_ids,
+                            const int64_t* block_table, void* partials,
+                            int32_t* counters,
+                            int64_t B, int64_t H_q, int64_t H_kv, int64_t D,
+                            int64_t page_size, int64_t n_pages,
+                            int64_t pool_page_stride, int64_t pool_head_stride,
+                            int64_t bt_stride, int64_t bt_width,
+                            int64_t n_slots, int64_t n_splits, int32_t* err,
+                            void* stream);
 
 /*
  * Varlen causal GQA attention over the paged pool for a packed batch of
@@ -134,6 +168,18 @@ int cie_mixed_attention(void* o, const void* q,
                         int64_t pool_page_stride, int64_t pool_head_stride,
                         int64_t bt_stride, int64_t bt_width, int64_t n_slots,
                         int32_t* err, void* stream);
+
+/*
+ * Measurement helper, no counterpart in the reference: reads n_chunks chunks
+ * of chunk_bytes (a multiple of 1024) at base + chunk_ids[i] * chunk_bytes and
+ * folds them into *sink (written only on an improbable hash), on
+ * n_workgroups workgroups of 256 threads.  Timed with shuffled ids and the KV
+ * page-head size it gives the HBM ceiling of the paged access pattern,
+ * without any attention math; bench.py reports it beside the decode figure.
+ */
+int cie_probe_gather_read(const void* base, const int32_t* chunk_ids,
+                          int64_t n_chunks, int64_t chunk_bytes,
+                          int64_t n_workgroups, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -3,7 +3,8 @@ import sys
 
 import torch
 
-from custom_inference_engine_amd import decode_gqa_attention, kv_append_decode, kv_append_tokens, mixed_gqa_attention
+from custom_inference_engine_amd import (decode_append_gqa_attention, decode_gqa_attention, kv_append_decode,
+                                         kv_append_tokens, mixed_gqa_attention)
 from oracle import paged_attention as ref
 
 DEV = "cuda"
@@ -29,6 +30,16 @@ def gpu_decode_step(case, n_splits=None, err=None):
     kv_append_decode(kp, vp, c.k_new, c.v_new, c.slot_ids, c.lens_pool, c.block_table, err=err)
     o = decode_gqa_attention(c.q, kp, vp, c.attended, c.slot_ids, c.block_table,
                              num_programs=n_splits, err=err)
+    torch.cuda.synchronize()
+    return kp.cpu(), vp.cpu(), o[0].float().cpu()
+
+
+def gpu_decode_fused_step(case, n_splits=None, err=None):
+    """KV append fused into the decode launch; returns (k_pool, v_pool, o) on the CPU."""
+    c = case.to(DEV)
+    kp, vp = c.k_pool.clone(), c.v_pool.clone()
+    o = decode_append_gqa_attention(c.q, kp, vp, c.k_new, c.v_new, c.lens_pool, c.slot_ids,
+                                    c.block_table, num_programs=n_splits, err=err)
     torch.cuda.synchronize()
     return kp.cpu(), vp.cpu(), o[0].float().cpu()
 

@@ -21,7 +21,8 @@ def declared_functions():
 def test_header_declares_the_hot_path():
     names = declared_functions()
     for want in ("cie_kv_append_decode", "cie_kv_append_tokens", "cie_paged_decode",
-                 "cie_paged_decode_workspace_bytes", "cie_mixed_attention",
+                 "cie_paged_decode_append", "cie_paged_decode_max_splits",
+                 "cie_paged_decode_partials_bytes", "cie_mixed_attention",
                  "cie_mixed_workspace_bytes", "cie_abi_version", "cie_status_string"):
         assert want in names
 
@@ -48,15 +49,17 @@ def test_version_and_status_strings(native_lib):
 
 
 def test_workspace_sizes(native_lib):
-    # (B, H_q, S, D + 2) fp32 partial state
-    assert native_lib.cie_paged_decode_workspace_bytes(32, 14, 64, 16) == 32 * 14 * 16 * 66 * 4
-    assert native_lib.cie_paged_decode_workspace_bytes(-1, 14, 64, 16) == -1
+    # (B, H_q, S, D + 2) fp32 partial state, 256-byte aligned regions
+    n = native_lib.cie_paged_decode_partials_bytes(32, 14, 64, 16)
+    assert n >= 32 * 14 * 16 * 66 * 4 and n % 256 == 0
+    assert native_lib.cie_paged_decode_partials_bytes(-1, 14, 64, 16) == -1
+    assert native_lib.cie_paged_decode_max_splits() >= 16
     assert native_lib.cie_mixed_workspace_bytes(32, 2, 64) > 0
     assert native_lib.cie_mixed_workspace_bytes(32, 0, 64) == -1
 
 
 def _decode_args(**over):
-    a = dict(o=8, q=16, k=32, v=48, lens=64, slots=80, bt=96, ws=112, B=1, H_q=14, H_kv=2, D=64,
+    a = dict(o=8, q=16, k=32, v=48, lens=64, slots=80, bt=96, ws=112, ctr=128, B=1, H_q=14, H_kv=2, D=64,
              page_size=16, n_pages=64, page_stride=2048, head_stride=1024, bt_stride=64,
              bt_width=64, n_slots=2, n_splits=4)
     a.update(over)
@@ -66,7 +69,7 @@ def _decode_args(**over):
 def _call_decode(lib, a):
     # fake, never-dereferenced device addresses: these calls must fail validation on the host
     return lib.cie_paged_decode(a["o"], a["q"], a["k"], a["v"], a["lens"], a["slots"], a["bt"],
-                                a["ws"], a["B"], a["H_q"], a["H_kv"], a["D"], a["page_size"],
+                                a["ws"], a["ctr"], a["B"], a["H_q"], a["H_kv"], a["D"], a["page_size"],
                                 a["n_pages"], a["page_stride"], a["head_stride"], a["bt_stride"],
                                 a["bt_width"], a["n_slots"], a["n_splits"], None, None)
 
@@ -80,6 +83,8 @@ def _call_decode(lib, a):
     ({"H_q": 34, "H_kv": 2}, -2),      # more than 16 query heads per kv head
     ({"q": 18}, -1),                   # q not 16-byte aligned
     ({"lens": 0}, -1),                 # null index pointer
+    ({"ctr": 0}, -1),                  # split counters needed when n_splits > 1
+    ({"n_splits": 65}, -2),            # above the merge's split limit
 ])
 def test_decode_rejects_bad_arguments_without_launching(native_lib, over, code):
     assert _call_decode(native_lib, _decode_args(**over)) == code
@@ -87,6 +92,18 @@ def test_decode_rejects_bad_arguments_without_launching(native_lib, over, code):
 
 def test_decode_empty_batch_is_a_noop(native_lib):
     assert _call_decode(native_lib, _decode_args(B=0)) == 0
+
+
+def test_fused_decode_rejects_missing_new_rows(native_lib):
+    a = _decode_args()
+    rc = native_lib.cie_paged_decode_append(a["o"], a["q"], a["k"], a["v"], None, None, 128, 64, 128, 64,
+                                            a["lens"], a["slots"], a["bt"], a["ws"], a["ctr"], 1, 14, 2, 64, 16,
+                                            64, 2048, 1024, 64, 64, 2, 4, None, None)
+    assert rc == -1
+    rc = native_lib.cie_paged_decode_append(a["o"], a["q"], a["k"], a["v"], 16, 24, 128, 64, 128, 64,
+                                            a["lens"], a["slots"], a["bt"], a["ws"], a["ctr"], 1, 14, 2, 64, 16,
+                                            64, 2048, 1024, 64, 64, 2, 4, None, None)
+    assert rc == -1  # v_new not 16-byte aligned
 
 
 def test_append_and_mixed_reject_bad_arguments(native_lib):

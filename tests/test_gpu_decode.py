@@ -10,7 +10,7 @@ from custom_inference_engine_amd import decode_gqa_attention
 from oracle import inputs
 from tests.conftest import assert_attn_close
 from tests.golden.make_golden import INPUT_FIELDS, build_case, digest
-from tests.gpu_helpers import DEV, bits, err_word, gpu_decode_step, note, oracle_decode
+from tests.gpu_helpers import DEV, bits, err_word, gpu_decode_fused_step, gpu_decode_step, note, oracle_decode
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
@@ -112,3 +112,54 @@ def test_decode_rejects_cpu_tensors():
     with pytest.raises(RuntimeError, match="HIP device"):
         decode_gqa_attention(case.q, case.k_pool, case.v_pool, case.attended, case.slot_ids,
                              case.block_table, num_programs=2)
+
+
+# ----------------------------------------------------------------------------- fused append + decode
+
+@pytest.mark.parametrize("make,splits", [
+    (lambda: inputs.config1(), 4),
+    (lambda: inputs.config2(seed=0), None),
+    (lambda: inputs.config2(seed=3, fixed=False), 16),
+    (lambda: inputs.config4(), 16),
+    (lambda: inputs.make_case([0, 1, 14, 15, 16, 30, 31, 32, 47, 63, 64, 127], seed=27), 3),
+    (lambda: inputs.make_case([0, 1, 14, 15, 16, 30, 31, 32, 47, 63, 64, 127], seed=27), 1),
+    (lambda: inputs.make_case([5, 100, 333], seed=28, h_q=16, h_kv=1, d=128, page_size=32), 5),
+], ids=["cfg1", "cfg2", "cfg2var", "cfg4", "edges-p3", "edges-p1", "g16-d128-ps32"])
+def test_fused_append_decode(native_lib, make, splits):
+    case = make()
+    note(f"fused decode B={case.B} splits={splits}")
+    err = err_word()
+    kp, vp, o = gpu_decode_fused_step(case, n_splits=splits, err=err)
+    ko, vo = case.appended_pools()
+    assert torch.equal(bits(kp), bits(ko)) and torch.equal(bits(vp), bits(vo)), "append not bit-exact"
+    assert_attn_close(o, oracle_decode(case), what="fused decode")
+    assert int(err.item()) == 0
+
+
+def test_fused_matches_two_launch_path_bitwise(native_lib):
+    """One launch (append fused) == decode_update + decode op, bit for bit."""
+    case = inputs.make_case([7, 90, 1000, 4095], seed=29)
+    note("fused vs two-launch")
+    kf, vf, of = gpu_decode_fused_step(case, n_splits=4)
+    k2, v2, o2 = gpu_decode_step(case, n_splits=4)
+    assert torch.equal(bits(kf), bits(k2)) and torch.equal(bits(vf), bits(v2))
+    assert torch.equal(of, o2)
+
+
+def test_decode_counters_return_to_zero(native_lib):
+    """Every call leaves the arrival counters zero, so the buffer is reused without clearing."""
+    case = inputs.make_case([300, 1, 2000], seed=30)
+    note("split counters")
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    ctr = torch.zeros(case.B * 2, dtype=torch.int32, device=DEV)
+    outs = []
+    for splits in (7, 7, 3, 16):
+        o = decode_gqa_attention(c.q, kp, vp, c.attended, c.slot_ids, c.block_table,
+                                 num_programs=splits, counters=ctr)
+        outs.append(o.clone())
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(ctr) == 0
+    assert torch.equal(outs[0], outs[1])
+    for o in outs:
+        assert_attn_close(o[0].float().cpu(), oracle_decode(case), what="counters")

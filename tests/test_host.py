@@ -94,7 +94,8 @@ def test_mixed_validation_mirrors_reference_asserts():
 def test_ops_registered_with_fake_impls():
     from torch._subclasses.fake_tensor import FakeTensorMode
 
-    for name in ("gqa_decode_attention", "gqa_mixed_attention", "kv_append_decode", "kv_append_tokens"):
+    for name in ("gqa_decode_attention", "gqa_mixed_attention", "kv_append_decode", "kv_append_tokens",
+                 "gqa_decode_append_attention"):
         assert hasattr(torch.ops.inference, name)
     case = inputs.make_case([10, 20], seed=4)
     attended = case.attended
@@ -111,11 +112,14 @@ def test_ops_registered_with_fake_impls():
         assert out.shape == case.q.shape
     schema = str(torch.ops.inference.kv_append_decode.default._schema)
     assert "!) k_cache" in schema and "!) v_cache" in schema and "!) k," not in schema
+    schema = str(torch.ops.inference.gqa_decode_append_attention.default._schema)
+    assert "!) k_cache" in schema and "!) v_cache" in schema and "!) q," not in schema
 
 
 def test_default_split_policy():
-    assert core.default_decode_splits(32, 2) == 16
-    assert core.default_decode_splits(16, 2) == 32
+    # about one split workgroup per CU (256 on MI355X)
+    assert core.default_decode_splits(32, 2) == 4
+    assert core.default_decode_splits(16, 2) == 8
     assert core.default_decode_splits(1, 2) == core.DECODE_MAX_SPLITS
     assert core.default_decode_splits(4096, 2) == 1
 
