@@ -171,7 +171,7 @@ int cie_mixed_attention(void* o, const void* q,
 
 /*
  * Measurement helper, no counterpart in the reference: reads n_chunks chunks
- * of chunk_bytes (a multiple of 1024) at base + chunk_ids[i] * chunk_bytes and
+ * of chunk_bytes (1024, 2048 or 4096) at base + chunk_ids[i] * chunk_bytes and
  * folds them into *sink (written only on an improbable hash), on
  * n_workgroups workgroups of 256 threads.  Timed with shuffled ids and the KV
  * page-head size it gives the HBM ceiling of the paged access pattern,
