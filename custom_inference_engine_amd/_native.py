@@ -49,10 +49,11 @@ _SIGNATURES = {
          _c_i64p, _c_i64p, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
-    "cie_mixed_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "cie_mixed_partials_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "cie_mixed_counters": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "cie_mixed_attention": (
         ctypes.c_int,
-        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_ptr, _c_i64,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_ptr, _c_ptr, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
@@ -61,7 +62,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

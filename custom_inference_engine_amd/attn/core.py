@@ -18,7 +18,7 @@ accepted and ignored.  Validation mirrors the reference's asserts and raises
 Outputs are allocated with ``torch.empty`` on the current stream (under graph
 capture they come from the graph pool), split partials likewise; the decode
 kernels' arrival counters are one persistent, self-cleaning buffer per device
-(``decode_counters``).
+(``split_counters``).
 The decode op also has a fused form, ``inference::gqa_decode_append_attention``,
 that performs ``KVStorage.decode_update`` and the decode in one launch.
 """
@@ -61,13 +61,13 @@ _ctr_cache: dict[int, torch.Tensor] = {}
 _ctr_retired: list[torch.Tensor] = []
 
 
-def decode_counters(dev: torch.device, n: int) -> torch.Tensor:
-    """The device's persistent split-arrival counters (zeroed once, kept zero by the kernel).
+def split_counters(dev: torch.device, n: int) -> torch.Tensor:
+    """The device's persistent split-arrival counters (zeroed once, kept zero by the kernels).
 
-    The decode kernel's counters must be zero before a call and are left zero
-    by it, so one buffer serves every stream-ordered call on a device, graph
-    replays included, without a clearing launch.  Calls that can overlap in
-    time (different streams) must pass their own zeroed ``counters``.
+    The decode and mixed kernels' counters must be zero before a call and are
+    left zero by it, so one buffer serves every stream-ordered call on a
+    device, graph replays included, without a clearing launch.  Calls that can
+    overlap in time (different streams) must pass their own zeroed ``counters``.
     Replaced buffers stay alive: a captured graph may still point at them.
     """
     with _ctr_lock:
@@ -84,7 +84,7 @@ def _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters):
     partials = torch.empty(lib.cie_paged_decode_partials_bytes(B, H_q, D, P), dtype=torch.uint8,
                            device=dev)
     if counters is None:
-        counters = decode_counters(dev, B * H_kv)
+        counters = split_counters(dev, B * H_kv)
     _require(counters.dtype == torch.int32 and counters.numel() >= B * H_kv, "counters too small")
     return partials, counters
 
@@ -210,7 +210,7 @@ def _as_rows(x: torch.Tensor, h_kv: int, d: int) -> torch.Tensor:
 
 
 def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids, block_table,
-                        BLOCK_M=16, BLOCK_N=64, num_warps=4, wrap=None, err=None):
+                        BLOCK_M=16, BLOCK_N=64, num_warps=4, wrap=None, err=None, counters=None):
     """Varlen causal GQA attention over the paged pool (chunked prefill + decode).
 
     q: (1, total_T, H_q, D) fp16 contiguous; cu_seqlens (B+1,); kv_lens (B,) =
@@ -234,12 +234,16 @@ def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids,
     o = torch.empty_like(q)
     if B == 0 or total_T == 0 or int(max_seqlen) == 0:
         return o
-    ws = torch.empty(lib.cie_mixed_workspace_bytes(B, H_kv, D), dtype=torch.uint8, device=dev)
+    partials = torch.empty(lib.cie_mixed_partials_bytes(total_T, H_q, D), dtype=torch.uint8, device=dev)
+    n_ctr = lib.cie_mixed_counters(B, H_kv, int(max_seqlen))
+    if counters is None:
+        counters = split_counters(dev, n_ctr)
+    _require(counters.dtype == torch.int32 and counters.numel() >= n_ctr, "counters too small")
     _native.check(
         lib.cie_mixed_attention(
             o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
             cu_seqlens.data_ptr(), kv_lens.data_ptr(), slot_ids.data_ptr(), block_table.data_ptr(),
-            ws.data_ptr(), B, total_T, int(max_seqlen), H_q, H_kv, D, PAGE_SIZE, N_PAGES,
+            partials.data_ptr(), counters.data_ptr(), B, total_T, int(max_seqlen), H_q, H_kv, D, PAGE_SIZE, N_PAGES,
             k.stride(0), k.stride(1), block_table.stride(0), block_table.shape[1],
             block_table.shape[0], _native.ptr(err), _native.stream_handle(dev),
         ),

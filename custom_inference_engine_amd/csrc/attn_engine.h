@@ -133,12 +133,18 @@ struct SoftmaxAcc {
 // One 32-key step for NCT column tiles.  key0a / key0b = absolute index of the
 // first key of the pair's two tiles (the tiles need not be adjacent; an absent
 // second tile passes a key0b past every limit).  A column attends key j iff
-// j < lim[c] (per lane: causal / length limit of the lane's column).
+// j < lim[c] (per lane: causal / length limit of the lane's column);
+// mask_from (wave-uniform) is the smallest limit of any column, so steps whose
+// keys all lie below it skip the masking.
+//
+// VALU per column tile and step: the max runs on raw scores (the scale is
+// positive), exp2 takes fma(s, scale, -m), and the accumulator rescale is
+// skipped when no column's max moved (alpha == 1 exactly).
 template <int D, int NCT>
 __device__ __forceinline__ void attend_pair(SoftmaxAcc<D, NCT>& st, const KVPair<D>& kv,
                                             const f16x8 (&qop)[NCT][Geo<D>::KS], int key0a,
-                                            int key0b, const int (&lim)[NCT], float scale_log2,
-                                            int grp) {
+                                            int key0b, const int (&lim)[NCT], int mask_from,
+                                            float scale_log2, int grp) {
   constexpr int KS = Geo<D>::KS;
   constexpr int NT = Geo<D>::NT;
   f16x8 va[NT];
@@ -146,6 +152,7 @@ __device__ __forceinline__ void attend_pair(SoftmaxAcc<D, NCT>& st, const KVPair
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int e = 0; e < 8; ++e) va[nt][e] = kv.v[e][nt];
+  const bool masked = max(key0a, key0b) + 16 > mask_from;  // uniform
 
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
@@ -156,17 +163,24 @@ __device__ __forceinline__ void attend_pair(SoftmaxAcc<D, NCT>& st, const KVPair
       s1 = mfma16x16x32(kv.k[1][ks], qop[c][ks], s1);
     }
     float sc[8];
-    const int kba = key0a + 4 * grp;
-    const int kbb = key0b + 4 * grp;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      sc[r] = (kba + r < lim[c]) ? s0[r] * scale_log2 : kNegInf;
-      sc[4 + r] = (kbb + r < lim[c]) ? s1[r] * scale_log2 : kNegInf;
+      sc[r] = s0[r];
+      sc[4 + r] = s1[r];
+    }
+    if (masked) {
+      const int kba = key0a + 4 * grp;
+      const int kbb = key0b + 4 * grp;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (kba + r >= lim[c]) sc[r] = kNegInf;
+        if (kbb + r >= lim[c]) sc[4 + r] = kNegInf;
+      }
     }
     float mb = sc[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) mb = fmaxf(mb, sc[e]);
-    mb = col_max4(mb);
+    mb = col_max4(mb) * scale_log2;
     const float m_new = fmaxf(st.m[c], mb);
     // A column with every key masked so far keeps m = -inf, l = 0, acc = 0;
     // m_use keeps exp2 away from (-inf) - (-inf).
@@ -176,21 +190,23 @@ __device__ __forceinline__ void attend_pair(SoftmaxAcc<D, NCT>& st, const KVPair
     float ps = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float pe = fast_exp2(sc[e] - m_use);
+      const float pe = fast_exp2(__builtin_fmaf(sc[e], scale_log2, -m_use));
       ps += pe;
       pop[e] = (f16)pe;
     }
-    st.l[c] = st.l[c] * alpha + ps;
+    st.l[c] = __builtin_fmaf(st.l[c], alpha, ps);
     st.m[c] = m_new;
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      f32x4 a = st.acc[c][nt];
-      a[0] *= alpha;
-      a[1] *= alpha;
-      a[2] *= alpha;
-      a[3] *= alpha;
-      st.acc[c][nt] = mfma16x16x32(va[nt], pop, a);
+      for (int nt = 0; nt < NT; ++nt) {
+        st.acc[c][nt][0] *= alpha;
+        st.acc[c][nt][1] *= alpha;
+        st.acc[c][nt][2] *= alpha;
+        st.acc[c][nt][3] *= alpha;
+      }
     }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) st.acc[c][nt] = mfma16x16x32(va[nt], pop, st.acc[c][nt]);
   }
 }
 
@@ -225,8 +241,14 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
   // Keys past this wave's range belong to another wave (or do not exist):
   // the zero-filled second tile of an odd-length range must score -inf.
   int lim_w[NCT];
+  int mask_from = t_end * 16;
 #pragma unroll
-  for (int c = 0; c < NCT; ++c) lim_w[c] = min(lim[c], t_end * 16);
+  for (int c = 0; c < NCT; ++c) {
+    lim_w[c] = min(lim[c], t_end * 16);
+    mask_from = min(mask_from, lim_w[c]);
+  }
+  // smallest limit over the wave's columns (wave-uniform)
+  for (int off = 1; off < kWave; off <<= 1) mask_from = min(mask_from, __shfl_xor(mask_from, off, kWave));
   KVPair<D> cur, nxt;
   auto fetch = [&](KVPair<D>& kv, int t) {
     const bool two = t + 1 < t_end;
@@ -241,7 +263,7 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
   for (int t = t_begin; t < t_end; t += 2) {
     if (t + 2 < t_end) fetch(nxt, t + 2);
     if ((t + 2) * 16 > key_end) zero_tail_rows<D>(cur, t * 16, t * 16 + 16, key_end, grp);
-    attend_pair<D, NCT>(st, cur, qop, t * 16, t * 16 + 16, lim_w, scale_log2, grp);
+    attend_pair<D, NCT>(st, cur, qop, t * 16, t * 16 + 16, lim_w, mask_from, scale_log2, grp);
     cur = nxt;
   }
 }

@@ -51,6 +51,30 @@ __device__ __forceinline__ void set_err(int32_t* err, int bit) {
 #endif
 }
 
+// Device-coherent (agent-scope) accesses: global_store / global_load with sc1,
+// visible across workgroups on every XCD once the store has completed
+// (s_waitcnt vmcnt(0)), with no L2 writeback / invalidate.
+__device__ __forceinline__ void agent_store(float* ptr, float v) {
+  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float agent_load(const float* ptr) {
+  return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// Last-arriver election: every workgroup of a group calls this once after its
+// partial results are stored with agent_store; exactly one (the last) gets
+// true.  Resetting the counter to zero is up to the winner.
+__device__ __forceinline__ bool arrive_last(int32_t* counter, int n_members, int* sm_flag) {
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *sm_flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               n_members - 1;
+  __syncthreads();
+  return *sm_flag != 0;
+}
+
 // Uniform (wave-invariant) value hint: lets the compiler keep it in an SGPR.
 __device__ __forceinline__ int uniform(int x) {
   return __builtin_amdgcn_readfirstlane(x);

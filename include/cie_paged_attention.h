@@ -152,16 +152,22 @@ int cie_paged_decode_append(void* o, const void* q, void* k_pool, void* v_pool,
  * mixed_gqa_attention_kernel (kernels/prefill_attention.py:10-198).
  *   q, o       : (total_T, H_q, D) dense fp16
  *   max_seqlen : upper bound on every sequence's query length (the
- *                reference's metadata token-count bucket); sizes the grid
- *   workspace  : cie_mixed_workspace_bytes(B, H_kv, D) bytes, any contents
- *                (split-KV partial state of short-query sequences)
+ *                reference's metadata token-count bucket); rows past it are
+ *                not computed (CIE_ERRBIT_LEN).  B <= 1024.
+ *   partials   : cie_mixed_partials_bytes(total_T, H_q, D) bytes, 16-byte
+ *                aligned, any contents (per-chunk softmax state)
+ *   counters   : cie_mixed_counters(B, H_kv, max_seqlen) int32, 16-byte
+ *                aligned, zero before the call and left zero by it (one
+ *                arrival counter per query tile; the same buffer can serve
+ *                cie_paged_decode, calls being stream-ordered)
  */
-int64_t cie_mixed_workspace_bytes(int64_t B, int64_t H_kv, int64_t D);
+int64_t cie_mixed_partials_bytes(int64_t total_T, int64_t H_q, int64_t D);
+int64_t cie_mixed_counters(int64_t B, int64_t H_kv, int64_t max_seqlen);
 int cie_mixed_attention(void* o, const void* q,
                         const void* k_pool, const void* v_pool,
                         const int64_t* cu_seqlens, const int64_t* kv_lens,
                         const int64_t* slot_ids, const int64_t* block_table,
-                        void* workspace,
+                        void* partials, int32_t* counters,
                         int64_t B, int64_t total_T, int64_t max_seqlen,
                         int64_t H_q, int64_t H_kv, int64_t D,
                         int64_t page_size, int64_t n_pages,

@@ -23,7 +23,8 @@ def test_header_declares_the_hot_path():
     for want in ("cie_kv_append_decode", "cie_kv_append_tokens", "cie_paged_decode",
                  "cie_paged_decode_append", "cie_paged_decode_max_splits",
                  "cie_paged_decode_partials_bytes", "cie_mixed_attention",
-                 "cie_mixed_workspace_bytes", "cie_abi_version", "cie_status_string"):
+                 "cie_mixed_partials_bytes", "cie_mixed_counters", "cie_abi_version",
+                 "cie_status_string"):
         assert want in names
 
 
@@ -54,8 +55,9 @@ def test_workspace_sizes(native_lib):
     assert n >= 32 * 14 * 16 * 66 * 4 and n % 256 == 0
     assert native_lib.cie_paged_decode_partials_bytes(-1, 14, 64, 16) == -1
     assert native_lib.cie_paged_decode_max_splits() >= 16
-    assert native_lib.cie_mixed_workspace_bytes(32, 2, 64) > 0
-    assert native_lib.cie_mixed_workspace_bytes(32, 0, 64) == -1
+    assert native_lib.cie_mixed_partials_bytes(1052, 14, 64) >= 1052 * 14 * 16 * 66 * 4
+    assert native_lib.cie_mixed_partials_bytes(10, 0, 64) == -1
+    assert native_lib.cie_mixed_counters(32, 2, 256) == 32 * 2 * 16
 
 
 def _decode_args(**over):
@@ -117,5 +119,8 @@ def test_append_and_mixed_reject_bad_arguments(native_lib):
     assert lib.cie_kv_append_decode(8, 8, 8, 8, 64, 64, 64, 64, 8, 8, 8, 1, 2, 16, 64, 10, 2048,
                                     1024, 4, 8, 2, None, None) == -1  # bt_stride < bt_width
     # mixed: G = 14 > 8 is outside the built set
-    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, 1, 4, 4, 14, 1, 64, 16, 10,
+    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, 32, 1, 4, 4, 14, 1, 64, 16, 10,
                                    1024, 1024, 10, 10, 2, None, None) == -2
+    # mixed: counters are required
+    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, None, 1, 4, 4, 14, 2, 64, 16, 10,
+                                   1024, 1024, 10, 10, 2, None, None) == -1

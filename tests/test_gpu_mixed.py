@@ -89,10 +89,12 @@ def test_mixed_leaves_rows_outside_sequences_untouched(native_lib):
     q[:, :case.T] = c.q
     o = torch.full_like(q, 7.0)
     lib = _native.load()
-    ws = torch.empty(lib.cie_mixed_workspace_bytes(case.B, 2, 64), dtype=torch.uint8, device=DEV)
+    ws = torch.empty(lib.cie_mixed_partials_bytes(T_pad, 14, 64), dtype=torch.uint8, device=DEV)
+    ctr = torch.zeros(lib.cie_mixed_counters(case.B, 2, 16), dtype=torch.int32, device=DEV)
     rc = lib.cie_mixed_attention(o.data_ptr(), q.data_ptr(), kp.data_ptr(), vp.data_ptr(),
                                  c.cu_seqlens.data_ptr(), c.kv_lens.data_ptr(), c.slot_ids.data_ptr(),
-                                 c.block_table.data_ptr(), ws.data_ptr(), case.B, T_pad, 16, 14, 2, 64,
+                                 c.block_table.data_ptr(), ws.data_ptr(), ctr.data_ptr(), case.B, T_pad,
+                                 16, 14, 2, 64,
                                  16, kp.shape[0], kp.stride(0), kp.stride(1), c.block_table.stride(0),
                                  c.block_table.shape[1], c.block_table.shape[0], None,
                                  _native.stream_handle(torch.device(DEV)))
@@ -108,3 +110,19 @@ def test_mixed_rows_beyond_max_seqlen_are_flagged(native_lib):
     err = err_word()
     gpu_mixed_step(case, max_seqlen=16, err=err)
     assert int(err.item()) & 2
+
+
+def test_mixed_counters_return_to_zero(native_lib):
+    """Multi-chunk tiles (long prefixes) leave their arrival counters zero."""
+    case = inputs.make_case([3000, 0, 2500, 700], [40, 1, 1, 18], seed=36)
+    note("mixed counters")
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    from custom_inference_engine_amd import mixed_gqa_attention
+    ctr = torch.zeros(case.B * 2 * 3, dtype=torch.int32, device=DEV)
+    for _ in range(2):
+        o = mixed_gqa_attention(c.q, kp, vp, 40, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
+                                counters=ctr)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(ctr) == 0
+    _check(case, o[0].float().cpu(), "mixed counters")
