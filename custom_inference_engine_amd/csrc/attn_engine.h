@@ -132,82 +132,119 @@ struct SoftmaxAcc {
 
 // One 32-key step for NCT column tiles.  key0a / key0b = absolute index of the
 // first key of the pair's two tiles (the tiles need not be adjacent; an absent
-// second tile passes a key0b past every limit).  A column attends key j iff
-// j < lim[c] (per lane: causal / length limit of the lane's column);
-// mask_from (wave-uniform) is the smallest limit of any column, so steps whose
-// keys all lie below it skip the masking.
+// second tile passes kNoKey).  A column attends key j iff j < lim[c] (per
+// lane: causal / length limit of the lane's column); mask_from (wave-uniform)
+// is the smallest limit of any column, so steps whose keys all lie below it
+// skip the masking.
 //
-// VALU per column tile and step: the max runs on raw scores (the scale is
-// positive), exp2 takes fma(s, scale, -m), and the accumulator rescale is
-// skipped when no column's max moved (alpha == 1 exactly).
-template <int D, int NCT>
-__device__ __forceinline__ void attend_pair(SoftmaxAcc<D, NCT>& st, const KVPair<D>& kv,
-                                            const f16x8 (&qop)[NCT][Geo<D>::KS], int key0a,
-                                            int key0b, const int (&lim)[NCT], int mask_from,
-                                            float scale_log2, int grp) {
+// The column tiles go in batches of up to kAttendBatch; a batch runs in
+// phases — its Q.K^T MFMAs, its columns' softmax updates, one (rare) rescale,
+// its P.V MFMAs — with no branch inside a phase, so one wave overlaps a column
+// tile's softmax with the MFMAs of the others.  VALU per column tile: the max
+// runs on raw scores (the scale is positive), exp2 takes fma(s, scale, -m),
+// and the accumulator rescale is skipped when no column's max moved
+// (alpha == 1 exactly).
+#ifndef CIE_ATTEND_BATCH
+#define CIE_ATTEND_BATCH 4
+#endif
+constexpr int kAttendBatch = CIE_ATTEND_BATCH;
+
+template <int D, int NCT, bool MASK>
+__device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const KVPair<D>& kv,
+                                                 const f16x8 (&qop)[NCT][Geo<D>::KS], int key0a,
+                                                 int key0b, const int (&lim)[NCT],
+                                                 float scale_log2, int grp) {
   constexpr int KS = Geo<D>::KS;
   constexpr int NT = Geo<D>::NT;
+  constexpr int SB = NCT < kAttendBatch ? NCT : kAttendBatch;
   f16x8 va[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int e = 0; e < 8; ++e) va[nt][e] = kv.v[e][nt];
-  const bool masked = max(key0a, key0b) + 16 > mask_from;  // uniform
 
 #pragma unroll
-  for (int c = 0; c < NCT; ++c) {
-    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < NCT; c0 += SB) {
+    f32x4 s[SB][2];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      s0 = mfma16x16x32(kv.k[0][ks], qop[c][ks], s0);
-      s1 = mfma16x16x32(kv.k[1][ks], qop[c][ks], s1);
-    }
-    float sc[8];
+    for (int i = 0; i < SB; ++i) {
+      if (c0 + i < NCT) {
+        s[i][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+        s[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sc[r] = s0[r];
-      sc[4 + r] = s1[r];
-    }
-    if (masked) {
-      const int kba = key0a + 4 * grp;
-      const int kbb = key0b + 4 * grp;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (kba + r >= lim[c]) sc[r] = kNegInf;
-        if (kbb + r >= lim[c]) sc[4 + r] = kNegInf;
+        for (int ks = 0; ks < KS; ++ks) {
+          s[i][0] = mfma16x16x32(kv.k[0][ks], qop[c0 + i][ks], s[i][0]);
+          s[i][1] = mfma16x16x32(kv.k[1][ks], qop[c0 + i][ks], s[i][1]);
+        }
       }
     }
-    float mb = sc[0];
+    f16x8 pop[SB];
+    float alpha[SB];
+    bool moved = false;
 #pragma unroll
-    for (int e = 1; e < 8; ++e) mb = fmaxf(mb, sc[e]);
-    mb = col_max4(mb) * scale_log2;
-    const float m_new = fmaxf(st.m[c], mb);
-    // A column with every key masked so far keeps m = -inf, l = 0, acc = 0;
-    // m_use keeps exp2 away from (-inf) - (-inf).
-    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-    const float alpha = fast_exp2(st.m[c] - m_use);
-    f16x8 pop;
-    float ps = 0.f;
+    for (int i = 0; i < SB; ++i) {
+      if (c0 + i < NCT) {
+        const int c = c0 + i;
+        float sc[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float pe = fast_exp2(__builtin_fmaf(sc[e], scale_log2, -m_use));
-      ps += pe;
-      pop[e] = (f16)pe;
-    }
-    st.l[c] = __builtin_fmaf(st.l[c], alpha, ps);
-    st.m[c] = m_new;
-    if (__any(alpha != 1.f)) {
+        for (int r = 0; r < 4; ++r) {
+          sc[r] = s[i][0][r];
+          sc[4 + r] = s[i][1][r];
+        }
+        if constexpr (MASK) {
+          const int kba = key0a + 4 * grp;
+          const int kbb = key0b + 4 * grp;
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        st.acc[c][nt][0] *= alpha;
-        st.acc[c][nt][1] *= alpha;
-        st.acc[c][nt][2] *= alpha;
-        st.acc[c][nt][3] *= alpha;
+          for (int r = 0; r < 4; ++r) {
+            sc[r] = kba + r < lim[c] ? sc[r] : kNegInf;
+            sc[4 + r] = kbb + r < lim[c] ? sc[4 + r] : kNegInf;
+          }
+        }
+        float mb = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                         fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        mb = col_max4(mb) * scale_log2;
+        const float m_new = fmaxf(st.m[c], mb);
+        // A column with every key masked so far keeps m = -inf, l = 0,
+        // acc = 0; m_use keeps exp2 away from (-inf) - (-inf).
+        const float m_use = (m_new == kNegInf) ? 0.f : m_new;
+        alpha[i] = fast_exp2(st.m[c] - m_use);
+        moved |= alpha[i] != 1.f;
+        float ps = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pe = fast_exp2(__builtin_fmaf(sc[e], scale_log2, -m_use));
+          ps += pe;
+          pop[i][e] = (f16)pe;
+        }
+        st.l[c] = __builtin_fmaf(st.l[c], alpha[i], ps);
+        st.m[c] = m_new;
       }
     }
+    if (__any(moved)) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) st.acc[c][nt] = mfma16x16x32(va[nt], pop, st.acc[c][nt]);
+      for (int i = 0; i < SB; ++i)
+        if (c0 + i < NCT)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) st.acc[c0 + i][nt] *= alpha[i];
+    }
+#pragma unroll
+    for (int i = 0; i < SB; ++i)
+      if (c0 + i < NCT)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          st.acc[c0 + i][nt] = mfma16x16x32(va[nt], pop[i], st.acc[c0 + i][nt]);
   }
+}
+
+template <int D, int NCT>
+__device__ __forceinline__ void attend_pair(SoftmaxAcc<D, NCT>& st, const KVPair<D>& kv,
+                                            const f16x8 (&qop)[NCT][Geo<D>::KS], int key0a,
+                                            int key0b, const int (&lim)[NCT], int mask_from,
+                                            float scale_log2, int grp) {
+  if (max(key0a, key0b) + 16 > mask_from)  // uniform
+    attend_pair_body<D, NCT, true>(st, kv, qop, key0a, key0b, lim, scale_log2, grp);
+  else
+    attend_pair_body<D, NCT, false>(st, kv, qop, key0a, key0b, lim, scale_log2, grp);
 }
 
 // Output dim held by (grp, r, nt) of the P.V accumulator.
@@ -228,43 +265,67 @@ struct PagedSrc {
   int32_t* err;
 };
 
-// Stream key tiles [t_begin, t_end) through attend_pair, two tiles per step,
-// with the next step's loads issued before the current step's math.
+// Stream key tiles [t_begin, t_end) of one wave through attend_pair, two
+// tiles per step.  The page ids of up to 64 tiles are gathered first, one per
+// lane, so a step's K/V loads depend on no other load; a ring of PF + 1
+// register-staged steps keeps PF steps of loads in flight ahead of the math.
 // key_end = number of keys that exist (rows at or past it are zeroed).
-template <int D, int NCT>
+template <int D, int NCT, int PF>
 __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
                                              const f16x8 (&qop)[NCT][Geo<D>::KS],
                                              const int (&lim)[NCT], int t_begin, int t_end,
                                              int key_end, const PagedSrc& src, float scale_log2,
                                              int r16, int grp) {
   if (t_begin >= t_end) return;
-  // Keys past this wave's range belong to another wave (or do not exist):
-  // the zero-filled second tile of an odd-length range must score -inf.
-  int lim_w[NCT];
-  int mask_from = t_end * 16;
+  int mask_from = kNoKey;
 #pragma unroll
-  for (int c = 0; c < NCT; ++c) {
-    lim_w[c] = min(lim[c], t_end * 16);
-    mask_from = min(mask_from, lim_w[c]);
-  }
+  for (int c = 0; c < NCT; ++c) mask_from = min(mask_from, lim[c]);
   // smallest limit over the wave's columns (wave-uniform)
   for (int off = 1; off < kWave; off <<= 1) mask_from = min(mask_from, __shfl_xor(mask_from, off, kWave));
-  KVPair<D> cur, nxt;
-  auto fetch = [&](KVPair<D>& kv, int t) {
-    const bool two = t + 1 < t_end;
-    const TileLoc l0 =
-        tile_loc(src.bt_row, t, src.page_size, src.n_pages, src.page_stride, src.head_off, D, src.err);
-    const TileLoc l1 = two ? tile_loc(src.bt_row, t + 1, src.page_size, src.n_pages,
-                                      src.page_stride, src.head_off, D, src.err)
-                           : l0;
-    load_pair<D>(kv, src.k_pool, src.v_pool, l0, l1, two, r16, grp);
-  };
-  fetch(cur, t_begin);
-  for (int t = t_begin; t < t_end; t += 2) {
-    if (t + 2 < t_end) fetch(nxt, t + 2);
-    if ((t + 2) * 16 > key_end) zero_tail_rows<D>(cur, t * 16, t * 16 + 16, key_end, grp);
-    attend_pair<D, NCT>(st, cur, qop, t * 16, t * 16 + 16, lim_w, mask_from, scale_log2, grp);
-    cur = nxt;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int tpp = src.page_size >> 4;  // 16-key tiles per page
+  for (int c0 = t_begin; c0 < t_end; c0 += kWave) {
+    const int n_chunk = min(kWave, t_end - c0);
+    int page = 0;
+    if (lane < n_chunk) {
+      int64_t pg = src.bt_row[(c0 + lane) / tpp];
+      if (pg < 0 || pg >= src.n_pages) {
+        set_err(src.err, CIE_ERRBIT_PAGE);
+        pg = 0;
+      }
+      page = (int)pg;
+    }
+    const int n_pairs = (n_chunk + 1) >> 1;
+    KVPair<D> ring[PF + 1];
+    int keya[PF + 1], keyb[PF + 1];
+    auto issue = [&](int slot, int j) {
+      const int ka = 2 * j;  // chunk-local index of the step's first tile
+      const bool two = ka + 1 < n_chunk;
+      const int ta = c0 + ka;
+      const int pa = __builtin_amdgcn_readlane(page, ka);
+      const int pb = two ? __builtin_amdgcn_readlane(page, ka + 1) : pa;
+      const TileLoc l0{(int64_t)pa * src.page_stride + src.head_off + (int64_t)((ta % tpp) * 16) * D};
+      const TileLoc l1{(int64_t)pb * src.page_stride + src.head_off +
+                       (int64_t)(((ta + 1) % tpp) * 16) * D};
+      keya[slot] = ta * 16;
+      keyb[slot] = two ? ta * 16 + 16 : kNoKey;
+      load_pair<D>(ring[slot], src.k_pool, src.v_pool, l0, l1, two, r16, grp);
+    };
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+      if (j < n_pairs) issue(j, j);
+    for (int j0 = 0; j0 < n_pairs; j0 += PF + 1) {
+#pragma unroll
+      for (int u = 0; u <= PF; ++u) {
+        const int j = j0 + u;
+        if (j < n_pairs) {
+          if (j + PF < n_pairs) issue((u + PF) % (PF + 1), j + PF);
+          const int ka = keya[u], kb = keyb[u];
+          if ((kb == kNoKey ? ka : kb) + 16 > key_end) zero_tail_rows<D>(ring[u], ka, kb, key_end, grp);
+          attend_pair<D, NCT>(st, ring[u], qop, ka, kb, lim, mask_from, scale_log2, grp);
+        }
+      }
+    }
   }
 }
 

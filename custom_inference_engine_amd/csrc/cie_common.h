@@ -19,9 +19,11 @@ constexpr int kWave = 64;
 // log2(e): softmax runs in the exp2 domain; scores are pre-multiplied by it.
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
+// Key index of an absent tile: past every limit, so all its scores are masked.
+constexpr int kNoKey = 0x3fffffff;
 
 __device__ __forceinline__ float fast_exp2(float x) {
-  // v_exp_f32: exact 2^x for x = -inf (gives 0), full-rate transcendental.
+  // v_exp_f32 (a quarter-rate transcendental): 2^x, exactly 0 at x = -inf.
   return __builtin_amdgcn_exp2f(x);
 }
 
@@ -30,15 +32,34 @@ __device__ __forceinline__ float lane_xor(float x, int m) {
   return __shfl_xor(x, m, kWave);
 }
 
+// The two values a lane sees after v_permlane16_swap / v_permlane32_swap of x
+// with itself: {x[l], x[l ^ 16]} and {x[l], x[l ^ 32]} (in some order).  Both
+// are VALU lane permutes on gfx950, no LDS round trip.
+__device__ __forceinline__ void swap16(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap32(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
 // max / sum over the four lanes {l, l^16, l^32, l^48}, i.e. over the lanes
-// that hold the same MFMA output column (l % 16).
+// that hold the same MFMA output column (l % 16).  Every lane of the four
+// gets the same bits (the two operands of each step are the same pair).
 __device__ __forceinline__ float col_max4(float x) {
-  x = fmaxf(x, lane_xor(x, 16));
-  return fmaxf(x, lane_xor(x, 32));
+  float a, b;
+  swap16(x, a, b);
+  swap32(fmaxf(a, b), a, b);
+  return fmaxf(a, b);
 }
 __device__ __forceinline__ float col_sum4(float x) {
-  x += lane_xor(x, 16);
-  return x + lane_xor(x, 32);
+  float a, b;
+  swap16(x, a, b);
+  swap32(a + b, a, b);
+  return a + b;
 }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
@@ -59,6 +80,26 @@ __device__ __forceinline__ void agent_store(float* ptr, float v) {
 }
 __device__ __forceinline__ float agent_load(const float* ptr) {
   return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16-byte device-coherent accesses: buffer_load / buffer_store_dwordx4 with
+// sc1 (the same cache policy as the agent-scope accesses above) through a
+// raw buffer resource over [base, base + bytes).  base must be wave-uniform.
+constexpr int kBufSc1 = 16;                  // cache-policy operand: sc1
+constexpr int kBufRsrcWord3 = 0x00020000;    // raw 32-bit buffer (gfx9 family)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  // readfirstlane yields an int: widen through uint32_t, never sign-extend
+  // the low word into the high one.
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const uint64_t u = ((uint64_t)hi << 32) | lo;
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), 0, (int)bytes, kBufRsrcWord3);
+}
+__device__ __forceinline__ void agent_store4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, kBufSc1);
+}
+__device__ __forceinline__ f32x4 agent_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kBufSc1));
 }
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 

@@ -12,52 +12,65 @@
 // BLOCK_M; grid (cdiv(max_seqlen, 16), H_kv, B), attn/core.py:90).  A tile's
 // work is laid out as (row, head) columns, G heads per row, packed 16 to an
 // MFMA column tile (attn_engine.h), so K/V bytes are shared by every head and
-// row of the tile inside the MFMA.  The tile's key range [0, kv_len + last row
-// + 1) is cut into up to kMaxChunks chunks, one workgroup each; the chunk's
-// key tiles are split over the workgroup's waves, and every wave carries all
-// of the tile's column tiles (in groups of kColGroup) for its keys, so each
-// K/V byte is loaded once per workgroup and reused by every column in
-// registers.  The waves fold their states through LDS one column tile at a
-// time.  Chunks are short for decode-like tiles (<= 16 columns, memory-bound)
-// and longer for prefill tiles (MFMA / VALU-bound), to bound partial traffic.
-// A tile with one chunk writes o directly.  Otherwise each chunk writes its
-// partial (m, l, acc) per column with device-coherent stores and the last
-// chunk to arrive (counter per tile) merges them with log-sum-exp, writes o
-// and resets the counter.  The reference instead walks a tile's whole prefix
-// with one program and pads every L = 1 sequence to a 16-row tile
+// row of the tile inside the MFMA.  One work item is (tile, column group,
+// key chunk): a column group is up to col_group<D>() column tiles, and a
+// tile's key range [0, kv_len + last row + 1) is cut into chunks only when it
+// is longer than kWavePairs 32-key steps per wave.  The item's key tiles are
+// split over the workgroup's waves; every wave carries all of the group's
+// column tiles, so each K/V byte is loaded once per workgroup and reused by
+// every column of the group in registers.  The waves fold their states
+// through LDS one column tile at a time.  A single-chunk item writes o
+// directly.  Otherwise each chunk writes its partial (m, l, acc) per column
+// with device-coherent stores and the last chunk to arrive (counter per
+// tile and column group) merges them with log-sum-exp, writes o and resets
+// the counter.  The reference instead walks a tile's whole prefix with one
+// program and pads every L = 1 sequence to a 16-row tile
 // (prefill_attention.py:49-50, 93).
 #include "attn_engine.h"
 
 namespace cie {
 
 // Build-time tuning (defaults are the shipped configuration):
-//   CIE_MIXED_CG           column tiles a wave carries at once (D = 64)
-//   CIE_MIXED_SHORT_PAIRS  32-key steps per chunk of a short (<= 16 column) tile
-//   CIE_MIXED_LONG_PAIRS   32-key steps per chunk of a prefill tile
+//   CIE_MIXED_WAVES        wavefronts per workgroup (D = 64)
+//   CIE_MIXED_CG           column tiles per work item (D = 64)
+//   CIE_MIXED_WAVE_PAIRS   32-key steps per wave before a tile's keys are
+//                          split over several workgroups
+//   CIE_MIXED_PF           32-key steps of loads in flight per wave (D = 64)
 //   CIE_MIXED_WG_PER_CU    workgroups per CU in the grid
+#ifndef CIE_MIXED_WAVES
+#define CIE_MIXED_WAVES 8
+#endif
 #ifndef CIE_MIXED_CG
-#define CIE_MIXED_CG 8
+#define CIE_MIXED_CG 2
 #endif
-#ifndef CIE_MIXED_SHORT_PAIRS
-#define CIE_MIXED_SHORT_PAIRS 16
+#ifndef CIE_MIXED_WAVE_PAIRS
+#define CIE_MIXED_WAVE_PAIRS 10
 #endif
-#ifndef CIE_MIXED_LONG_PAIRS
-#define CIE_MIXED_LONG_PAIRS 24
+#ifndef CIE_MIXED_PF
+#define CIE_MIXED_PF 2
 #endif
 #ifndef CIE_MIXED_WG_PER_CU
-#define CIE_MIXED_WG_PER_CU 2
+#define CIE_MIXED_WG_PER_CU 1
 #endif
 
-constexpr int kMixedWaves = 4;
-constexpr int kMaxChunks = 16;  // workgroups per query tile at most
-constexpr int kShortPairsPerChunk = CIE_MIXED_SHORT_PAIRS;
-constexpr int kLongPairsPerChunk = CIE_MIXED_LONG_PAIRS;
-constexpr int kMaxCols = 128;  // columns per tile: 16 rows x G <= 8 heads
+constexpr int kWavePairs = CIE_MIXED_WAVE_PAIRS;
+constexpr int kMaxChunks = 16;    // workgroups per (tile, column group) at most
+constexpr int kMaxColGroups = 8;  // column groups per tile at most (<= 8 column tiles)
 
-// Column tiles a wave carries at once (registers: 16*NT accumulators each).
+// Wavefronts per workgroup, column tiles per work item (registers: 16*NT
+// accumulators each) and load prefetch depth (registers: one 32-key K/V step
+// each).  D = 128 runs 4 waves (one per SIMD, so each may use 512 registers).
+template <int D>
+constexpr int mixed_waves() {
+  return D <= 64 ? CIE_MIXED_WAVES : 4;
+}
 template <int D>
 constexpr int col_group() {
-  return D <= 64 ? CIE_MIXED_CG : 2;
+  return D <= 64 ? CIE_MIXED_CG : 1;
+}
+template <int D>
+constexpr int mixed_pf() {
+  return D <= 64 ? CIE_MIXED_PF : 1;
 }
 
 struct MixedParams {
@@ -72,7 +85,7 @@ struct MixedParams {
   float* part_m;  // [total_T][H_q][kMaxChunks]
   float* part_l;
   float* part_acc;  // [total_T][H_q][kMaxChunks][D]
-  int32_t* counters;  // [B][H_kv][n_qtiles], zero between calls
+  int32_t* counters;  // [B][H_kv][n_qtiles][kMaxColGroups], zero between calls
   int64_t pool_page_stride, pool_head_stride, bt_stride, n_pages, total_T;
   int32_t bt_width, n_slots, B, H_q, H_kv, G, page_size, n_qtiles;
   float scale_log2;
@@ -109,23 +122,31 @@ __device__ __forceinline__ SeqInfo seq_info(const MixedParams& p, int b) {
 }
 
 struct TilePlan {
-  int row0, rows, n_combos, n_ctiles, key_end, n_ktiles, n_chunks;
-  bool shorttile;
+  int row0, rows, n_combos, n_ctiles, n_groups, key_end, n_ktiles, n_pairs, n_chunks;
 };
 
-__device__ __forceinline__ TilePlan tile_plan(int qt, const SeqInfo& s, int G) {
+// cg = column tiles per group, waves = wavefronts per workgroup.
+__device__ __forceinline__ TilePlan tile_plan(int qt, const SeqInfo& s, int G, int cg, int waves) {
   TilePlan t;
   t.row0 = qt * 16;
   t.rows = min(16, s.L - t.row0);
   t.n_combos = t.rows * G;
   t.n_ctiles = (t.n_combos + 15) >> 4;
+  t.n_groups = (t.n_ctiles + cg - 1) / cg;
   t.key_end = s.c + t.row0 + t.rows;
   t.n_ktiles = (t.key_end + 15) >> 4;
-  t.shorttile = t.n_ctiles == 1;
-  const int n_pairs = (t.n_ktiles + 1) >> 1;
-  const int per = t.shorttile ? kShortPairsPerChunk : kLongPairsPerChunk;
-  t.n_chunks = max(1, min(kMaxChunks, (n_pairs + per - 1) / per));
+  t.n_pairs = (t.n_ktiles + 1) >> 1;
+  const int per = waves * kWavePairs;
+  t.n_chunks = max(1, min(kMaxChunks, (t.n_pairs + per - 1) / per));
   return t;
+}
+
+// Key tiles [*t0, *t1) of part i of n when a tile's 32-key steps are split
+// into n near-equal runs (run boundaries on whole steps).
+__device__ __forceinline__ void split_steps(int t_begin, int t_end, int i, int n, int& t0, int& t1) {
+  const int steps = (t_end - t_begin + 1) >> 1;
+  t0 = min(t_end, t_begin + 2 * (int)((int64_t)steps * i / n));
+  t1 = min(t_end, t_begin + 2 * (int)((int64_t)steps * (i + 1) / n));
 }
 
 // Q^T operand and key limit of column tile ct (columns = (row, head) pairs).
@@ -149,71 +170,53 @@ __device__ __forceinline__ void load_combo_q(const MixedParams& p, const SeqInfo
   }
 }
 
-// Global (row, q head) index of column cc of the tile.
-__device__ __forceinline__ int64_t column_row(const MixedParams& p, const SeqInfo& s,
-                                              const TilePlan& tp, int g, int cc) {
+// Row of column cc of the tile relative to the tile's first row's first q
+// head, in units of (row, q head) = H_q * (row) + g * G + head - ...; i.e. the
+// index into [(t0 + row0) * H_q, ...) of the tile's partial / output rows.
+__device__ __forceinline__ int column_off(const MixedParams& p, int g, int cc) {
   const int row = cc / p.G;
   const int head = cc - row * p.G;
-  return (s.t0 + tp.row0 + row) * p.H_q + g * p.G + head;
+  return row * p.H_q + g * p.G + head;
 }
 
-// Last chunk of a tile: combine the n_chunks partials of every column into o.
-// A thread takes 16 consecutive dims of one column and issues all of its
-// chunk loads at once; m / l of every (column, chunk) are staged in LDS
-// (sm: >= 2 * kMaxCols * kMaxChunks floats).
+// Profiling builds only (-DCIE_MIXED_TRACE): thread 0 stamps each work item's
+// phases (s_memrealtime) into the buffer passed as `err`, 16 words per
+// (kv head, item).
+#ifdef CIE_MIXED_TRACE
+#define MIXED_TRACE(item, k, v)                                                                  \
+  do {                                                                                           \
+    if (threadIdx.x == 0 && p.err != nullptr && (item) < 4096) {                                 \
+      __builtin_amdgcn_s_waitcnt(0);                                                             \
+      reinterpret_cast<uint64_t*>(p.err)[((int64_t)blockIdx.y * 4096 + (item)) * 16 + (k)] = (v); \
+    }                                                                                            \
+  } while (0)
+#else
+#define MIXED_TRACE(item, k, v) \
+  do {                          \
+  } while (0)
+#endif
+
+// Where a tile's partial state lives: rows r = column_off(...) of the tile
+// (relative to row (t0 + row0) * H_q), chunk k.
+struct PartRegion {
+  __amdgpu_buffer_rsrc_t acc;  // over the tile's 16 * H_q * kMaxChunks * D floats
+  float* m;                    // tile-relative row 0 of part_m
+  float* l;
+};
+
 template <int D>
-__device__ __forceinline__ void merge_tile(const MixedParams& p, const SeqInfo& s,
-                                           const TilePlan& tp, int g, float* sm) {
-  const int K = tp.n_chunks;
-  float* sm_m = sm;
-  float* sm_l = sm + kMaxCols * kMaxChunks;
-  for (int i = threadIdx.x; i < tp.n_combos * K; i += kMixedWaves * kWave) {
-    const int cc = i / K;
-    const int k = i - cc * K;
-    const int64_t prow = column_row(p, s, tp, g, cc) * kMaxChunks + k;
-    sm_m[i] = agent_load(p.part_m + prow);
-    sm_l[i] = agent_load(p.part_l + prow);
-  }
-  __syncthreads();
-  constexpr int kSeg = 16;  // dims per thread
-  for (int it = threadIdx.x; it < tp.n_combos * (D / kSeg); it += kMixedWaves * kWave) {
-    const int cc = it / (D / kSeg);
-    const int d0 = (it - cc * (D / kSeg)) * kSeg;
-    const int64_t crow = column_row(p, s, tp, g, cc);
-    float M = kNegInf;
-    for (int k = 0; k < K; ++k) M = fmaxf(M, sm_m[cc * K + k]);
-    float num[kSeg] = {};
-    float den = 0.f;
-    // chunks in groups of 4: each group's loads are issued together
-    for (int k0 = 0; k0 < K; k0 += 4) {
-      float val[4][kSeg];
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int j = 0; j < kSeg; ++j)
-          val[u][j] = k0 + u < K ? agent_load(p.part_acc + (crow * kMaxChunks + k0 + u) * D + d0 + j)
-                                 : 0.f;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (k0 + u < K) {
-          const float mk = sm_m[cc * K + k0 + u];
-          const float a = mk == kNegInf ? 0.f : fast_exp2(mk - M);
-          den += a * sm_l[cc * K + k0 + u];
-#pragma unroll
-          for (int j = 0; j < kSeg; ++j) num[j] += a * val[u][j];
-        }
-      }
-    }
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    f16x8 out[kSeg / 8];
-#pragma unroll
-    for (int j = 0; j < kSeg; ++j) out[j >> 3][j & 7] = (f16)(num[j] * inv);
-#pragma unroll
-    for (int v = 0; v < kSeg / 8; ++v) reinterpret_cast<f16x8*>(p.o + crow * D + d0)[v] = out[v];
-  }
+__device__ __forceinline__ PartRegion part_region(const MixedParams& p, const SeqInfo& s,
+                                                  const TilePlan& tp) {
+  const int64_t row0 = (s.t0 + tp.row0) * p.H_q;
+  PartRegion r;
+  r.acc = coherent_rsrc(p.part_acc + row0 * kMaxChunks * D,
+                        (uint32_t)(16 * p.H_q * kMaxChunks * D * sizeof(float)));
+  r.m = p.part_m + row0 * kMaxChunks;
+  r.l = p.part_l + row0 * kMaxChunks;
+  return r;
 }
 
-// One wave's share of a chunk: key tiles [w0, w1) against column tiles
+// One work item's waves: key tiles [w0, w1) against column tiles
 // [ct0, ct0 + NCT); then the workgroup folds each column tile through LDS
 // and writes o (single chunk) or the chunk's partial state.
 template <int D, int NCT>
@@ -221,15 +224,21 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
                                           const TilePlan& tp, int g, int ct0, int chunk, int w0,
                                           int w1, const PagedSrc& src, int wave, int r16, int grp,
                                           float (*sm_m)[16], float (*sm_l)[16],
-                                          float (*sm_acc)[16][D + 1]) {
+                                          float (*sm_acc)[16][D + 4], int item) {
   constexpr int NT = Geo<D>::NT;
+  constexpr int W = mixed_waves<D>();
   f16x8 qop[NCT][Geo<D>::KS];
   int lim[NCT];
 #pragma unroll
   for (int c = 0; c < NCT; ++c) load_combo_q<D>(p, s, tp, g, ct0 + c, r16, grp, qop[c], lim[c]);
+  MIXED_TRACE(item, 9, __builtin_amdgcn_s_memrealtime());
   SoftmaxAcc<D, NCT> st;
   st.init();
-  stream_tiles<D, NCT>(st, qop, lim, w0, w1, tp.key_end, src, p.scale_log2, r16, grp);
+  stream_tiles<D, NCT, mixed_pf<D>()>(st, qop, lim, w0, w1, tp.key_end, src, p.scale_log2, r16,
+                                      grp);
+  MIXED_TRACE(item, 8, __builtin_amdgcn_s_memrealtime());
+  const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
+  const PartRegion pr = part_region<D>(p, s, tp);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const float l = col_sum4(st.l[c]);
@@ -238,111 +247,157 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
       sm_m[wave][r16] = st.m[c];
       sm_l[wave][r16] = l;
     }
+    // lane (r16, grp) holds dims NT * (4 * grp + r) + nt: 4 * NT contiguous floats
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sm_acc[wave][r16][acc_dim<D>(grp, r, nt)] = st.acc[c][nt][r];
+      for (int nq = 0; nq < NT / 4; ++nq)
+        *reinterpret_cast<f32x4*>(&sm_acc[wave][r16][NT * (4 * grp + r) + 4 * nq]) =
+            f32x4{st.acc[c][4 * nq][r], st.acc[c][4 * nq + 1][r], st.acc[c][4 * nq + 2][r],
+                  st.acc[c][4 * nq + 3][r]};
     __syncthreads();
     const int n_cols = min(16, tp.n_combos - (ct0 + c) * 16);
-    for (int it = threadIdx.x; it < n_cols * D; it += kMixedWaves * kWave) {
-      const int j = it / D;
-      const int d = it - j * D;
+    for (int it = threadIdx.x; it < n_cols * (D / 4); it += W * kWave) {
+      const int j = it / (D / 4);
+      const int d = (it - j * (D / 4)) * 4;
       float M = kNegInf;
 #pragma unroll
-      for (int w = 0; w < kMixedWaves; ++w) M = fmaxf(M, sm_m[w][j]);
-      float num = 0.f, den = 0.f;
+      for (int w = 0; w < W; ++w) M = fmaxf(M, sm_m[w][j]);
+      f32x4 num = {0.f, 0.f, 0.f, 0.f};
+      float den = 0.f;
 #pragma unroll
-      for (int w = 0; w < kMixedWaves; ++w) {
+      for (int w = 0; w < W; ++w) {
         const float mw = sm_m[w][j];
-        if (mw != kNegInf) {
-          const float a = fast_exp2(mw - M);
-          num += a * sm_acc[w][j][d];
-          den += a * sm_l[w][j];
-        }
+        const float a = mw == kNegInf ? 0.f : fast_exp2(mw - M);
+        num += a * *reinterpret_cast<const f32x4*>(&sm_acc[w][j][d]);
+        den = __builtin_fmaf(a, sm_l[w][j], den);
       }
-      const int64_t crow = column_row(p, s, tp, g, (ct0 + c) * 16 + j);
+      const int off = column_off(p, g, (ct0 + c) * 16 + j);
       if (tp.n_chunks == 1) {
-        p.o[crow * D + d] = (f16)(den > 0.f ? num / den : 0.f);
+        const float inv = den > 0.f ? 1.f / den : 0.f;
+        const f16x4 h = {(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
+                         (f16)(num[3] * inv)};
+        *reinterpret_cast<f16x4*>(p.o + (tile_row0 + off) * D + d) = h;
       } else {
-        const int64_t prow = crow * kMaxChunks + chunk;
-        agent_store(p.part_acc + prow * D + d, num);
+        const int prow = off * kMaxChunks + chunk;
+        agent_store4(pr.acc, (uint32_t)((prow * D + d) * sizeof(float)), num);
         if (d == 0) {
-          agent_store(p.part_m + prow, M);
-          agent_store(p.part_l + prow, den);
+          agent_store(pr.m + prow, M);
+          agent_store(pr.l + prow, den);
         }
       }
     }
   }
 }
 
+// Last chunk of a (tile, column group): combine the n_chunks partials of the
+// group's columns into o.  A thread takes 4 consecutive dims of one column
+// (consecutive threads: consecutive dims, so every load is a whole-line
+// 16-byte access) and walks the chunks in groups of four with a running
+// log-sum-exp, so each group's loads go out together.
+template <int D>
+__device__ __forceinline__ void merge_group(const MixedParams& p, const SeqInfo& s,
+                                            const TilePlan& tp, int g, int ct0, int n_cols) {
+  constexpr int kGroup = 4;
+  const int K = tp.n_chunks;
+  const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
+  const PartRegion pr = part_region<D>(p, s, tp);
+  for (int it = threadIdx.x; it < n_cols * (D / 4); it += mixed_waves<D>() * kWave) {
+    const int j = it / (D / 4);
+    const int d = (it - j * (D / 4)) * 4;
+    const int off = column_off(p, g, ct0 * 16 + j);
+    float M = kNegInf, den = 0.f;
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < K; k0 += kGroup) {
+      float mk[kGroup], lk[kGroup];
+      f32x4 val[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        const int prow = off * kMaxChunks + k0 + u;
+        if (k0 + u < K) {
+          mk[u] = agent_load(pr.m + prow);
+          lk[u] = agent_load(pr.l + prow);
+          val[u] = agent_load4(pr.acc, (uint32_t)((prow * D + d) * sizeof(float)));
+        } else {
+          mk[u] = kNegInf;
+          lk[u] = 0.f;
+          val[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      float Mg = M;
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) Mg = fmaxf(Mg, mk[u]);
+      if (Mg == kNegInf) continue;  // nothing attended so far
+      const float rs = fast_exp2(M - Mg);  // 0 when M = -inf
+      den *= rs;
+      num *= rs;
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        const float a = mk[u] == kNegInf ? 0.f : fast_exp2(mk[u] - Mg);
+        den = __builtin_fmaf(a, lk[u], den);
+        num += a * val[u];
+      }
+      M = Mg;
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    const f16x4 h = {(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
+                     (f16)(num[3] * inv)};
+    *reinterpret_cast<f16x4*>(p.o + (tile_row0 + off) * D + d) = h;
+  }
+}
+
 constexpr int kMaxSeqs = 1024;  // sequences a launch can plan (LDS prefix table)
 
-// Profiling builds only (-DCIE_MIXED_TRACE): thread 0 stamps each work item's
-// phases (s_memrealtime) into the buffer passed as `err`, 8 words per
-// (kv head, item).
-#ifdef CIE_MIXED_TRACE
-#define MIXED_TRACE(item, k, v)                                                                 \
-  do {                                                                                          \
-    if (threadIdx.x == 0 && p.err != nullptr && (item) < 4096) {                                \
-      __builtin_amdgcn_s_waitcnt(0);                                                            \
-      reinterpret_cast<uint64_t*>(p.err)[((int64_t)blockIdx.y * 4096 + (item)) * 8 + (k)] = (v); \
-    }                                                                                           \
-  } while (0)
-#else
-#define MIXED_TRACE(item, k, v) \
-  do {                          \
-  } while (0)
-#endif
-
-// Items of sequence s: sum over its (grid-covered) query tiles of the chunks.
-__device__ __forceinline__ int seq_items(const SeqInfo& s, int n_qtiles, int G) {
+// Items of sequence s: sum over its (grid-covered) query tiles of
+// column groups x chunks.
+__device__ __forceinline__ int seq_items(const SeqInfo& s, int n_qtiles, int G, int cg, int waves) {
   const int n_tiles = min((s.L + 15) >> 4, n_qtiles);
   int n = 0;
-  for (int qt = 0; qt < n_tiles; ++qt) n += tile_plan(qt, s, G).n_chunks;
+  for (int qt = 0; qt < n_tiles; ++qt) {
+    const TilePlan tp = tile_plan(qt, s, G, cg, waves);
+    n += tp.n_groups * tp.n_chunks;
+  }
   return n;
 }
 
-// One work item: chunk `chunk` of query tile qt of sequence b, kv head g.
+// One work item: column group gi, chunk `chunk` of query tile qt of sequence
+// b, kv head g.
 template <int D>
 __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo& s, int b, int g,
-                                             int qt, int chunk, float (*sm_m)[16],
-                                             float (*sm_l)[16], float (*sm_acc)[16][D + 1],
-                                             int* sm_last, int item) {
+                                             int qt, int j, float (*sm_m)[16], float (*sm_l)[16],
+                                             float (*sm_acc)[16][D + 4], int* sm_last, int item) {
   constexpr int CG = col_group<D>();
+  constexpr int W = mixed_waves<D>();
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int r16 = lane & 15;
   const int grp = lane >> 4;
-  const TilePlan tp = tile_plan(qt, s, p.G);
+  const TilePlan tp = tile_plan(qt, s, p.G, CG, W);
+  const int gi = j / tp.n_chunks;
+  const int chunk = j - gi * tp.n_chunks;
+  const int ct0 = gi * CG;
+  const int n = min(CG, tp.n_ctiles - ct0);
   // this chunk's key tiles, and this wave's share of them
-  const int kt0 = (int)((int64_t)tp.n_ktiles * chunk / tp.n_chunks);
-  const int kt1 = (int)((int64_t)tp.n_ktiles * (chunk + 1) / tp.n_chunks);
-  const int w0 = kt0 + (int)((int64_t)(kt1 - kt0) * wave / kMixedWaves);
-  const int w1 = kt0 + (int)((int64_t)(kt1 - kt0) * (wave + 1) / kMixedWaves);
+  int kt0, kt1, w0, w1;
+  split_steps(0, tp.n_ktiles, chunk, tp.n_chunks, kt0, kt1);
+  split_steps(kt0, kt1, wave, W, w0, w1);
   const PagedSrc src{p.k_pool,  p.v_pool,  p.block_table + s.slot * p.bt_stride,
                      (int64_t)g * p.pool_head_stride, p.pool_page_stride, p.n_pages,
                      p.page_size, p.err};
-
-  for (int ct0 = 0; ct0 < tp.n_ctiles; ct0 += CG) {
-    const int n = min(CG, tp.n_ctiles - ct0);
-    switch (n) {
+  switch (n) {
 #define CIE_GROUP_CASE(k)                                                                      \
   case k:                                                                                      \
     if constexpr (k <= CG)                                                                     \
-      run_group<D, k>(p, s, tp, g, ct0, chunk, w0, w1, src, wave, r16, grp, sm_m, sm_l, sm_acc); \
+      run_group<D, k>(p, s, tp, g, ct0, chunk, w0, w1, src, wave, r16, grp, sm_m, sm_l, sm_acc, \
+                      item);                                                                   \
     break;
-      CIE_GROUP_CASE(1)
-      CIE_GROUP_CASE(2)
-      CIE_GROUP_CASE(3)
-      CIE_GROUP_CASE(4)
-      CIE_GROUP_CASE(5)
-      CIE_GROUP_CASE(6)
-      CIE_GROUP_CASE(7)
-      CIE_GROUP_CASE(8)
+    CIE_GROUP_CASE(1)
+    CIE_GROUP_CASE(2)
+    CIE_GROUP_CASE(3)
+    CIE_GROUP_CASE(4)
 #undef CIE_GROUP_CASE
-      default:
-        break;
-    }
+    default:
+      break;
   }
   MIXED_TRACE(item, 2, __builtin_amdgcn_s_memrealtime());
   MIXED_TRACE(item, 5, (uint64_t)(tp.n_ctiles * 1000000 + tp.n_chunks * 10000 + (kt1 - kt0)));
@@ -351,11 +406,12 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
     MIXED_TRACE(item, 3, __builtin_amdgcn_s_memrealtime());
     return;
   }
-  // The last chunk of this tile to arrive merges all chunks.
-  int32_t* ctr = p.counters + ((int64_t)b * p.H_kv + g) * p.n_qtiles + qt;
+  // The last chunk of this (tile, column group) to arrive merges all chunks.
+  int32_t* ctr =
+      p.counters + (((int64_t)b * p.H_kv + g) * p.n_qtiles + qt) * kMaxColGroups + gi;
   if (arrive_last(ctr, tp.n_chunks, sm_last)) {
     MIXED_TRACE(item, 4, __builtin_amdgcn_s_memrealtime());
-    merge_tile<D>(p, s, tp, g, &sm_acc[0][0][0]);
+    merge_group<D>(p, s, tp, g, ct0, min(16 * n, tp.n_combos - 16 * ct0));
     if (threadIdx.x == 0) *ctr = 0;
   }
   __syncthreads();
@@ -365,19 +421,21 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
 // Grid (n_workgroups, H_kv): every workgroup plans the whole batch — per
 // sequence item counts and their prefix sums in LDS — and takes items
 // blockIdx.x, blockIdx.x + gridDim.x, ...  (items ordered by sequence, tile,
-// chunk), so no workgroup is launched for an empty (tile, chunk) slot.
+// column group, chunk), so no workgroup is launched for an empty slot.
 template <int D>
-__global__ __launch_bounds__(kMixedWaves * kWave) void mixed_attention_kernel(MixedParams p) {
-  static_assert(kMixedWaves * 16 * (D + 1) >= 2 * kMaxCols * kMaxChunks, "merge scratch");
-  __shared__ float sm_m[kMixedWaves][16];
-  __shared__ float sm_l[kMixedWaves][16];
-  __shared__ float sm_acc[kMixedWaves][16][D + 1];
+__global__ __launch_bounds__(mixed_waves<D>() * kWave) void mixed_attention_kernel(MixedParams p) {
+  static_assert(col_group<D>() <= 4 && 8 / col_group<D>() <= kMaxColGroups, "column groups");
+  constexpr int W = mixed_waves<D>();
+  constexpr int NTH = W * kWave;
+  __shared__ float sm_m[W][16];
+  __shared__ float sm_l[W][16];
+  __shared__ __attribute__((aligned(16))) float sm_acc[W][16][D + 4];
   __shared__ int sm_last;
   __shared__ int sm_prefix[kMaxSeqs + 1];
-  __shared__ int sm_scan[kMixedWaves * kWave];
+  __shared__ int sm_scan[NTH];
 
+  constexpr int CG = col_group<D>();
   const int g = blockIdx.y;
-  constexpr int NTH = kMixedWaves * kWave;
   // Per-thread item counts of sequences b = tid, tid + NTH, ... (B <= kMaxSeqs).
   int base = 0;
   for (int b0 = 0; b0 < p.B; b0 += NTH) {
@@ -387,7 +445,7 @@ __global__ __launch_bounds__(kMixedWaves * kWave) void mixed_attention_kernel(Mi
       const SeqInfo s = seq_info(p, b);
       if (g == 0 && blockIdx.x == 0 && ((s.L + 15) >> 4) > p.n_qtiles)
         set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
-      n = s.L > 0 ? seq_items(s, p.n_qtiles, p.G) : 0;
+      n = s.L > 0 ? seq_items(s, p.n_qtiles, p.G, CG, W) : 0;
     }
     // inclusive block scan of n
     sm_scan[threadIdx.x] = n;
@@ -421,9 +479,10 @@ __global__ __launch_bounds__(kMixedWaves * kWave) void mixed_attention_kernel(Mi
     int j = item - sm_prefix[b];
     int qt = 0;
     for (;; ++qt) {
-      const int nc = tile_plan(qt, s, p.G).n_chunks;
-      if (j < nc) break;
-      j -= nc;
+      const TilePlan tp = tile_plan(qt, s, p.G, CG, W);
+      const int nt = tp.n_groups * tp.n_chunks;
+      if (j < nt) break;
+      j -= nt;
     }
     MIXED_TRACE(item, 1, __builtin_amdgcn_s_memrealtime());
     MIXED_TRACE(item, 7, (uint64_t)(b * 1000 + qt));
@@ -431,7 +490,7 @@ __global__ __launch_bounds__(kMixedWaves * kWave) void mixed_attention_kernel(Mi
   }
 }
 
-// Workgroups of the mixed grid: about two per CU over the kv heads.
+// Workgroups of the mixed grid: CIE_MIXED_WG_PER_CU per CU over the kv heads.
 static int mixed_workgroups(int H_kv) {
   int dev = 0, n_cu = 256;
   if (hipGetDevice(&dev) == hipSuccess)
@@ -443,7 +502,7 @@ static int mixed_workgroups(int H_kv) {
 template <int D>
 static int launch_mixed(const MixedParams& p, hipStream_t stream) {
   dim3 grid(mixed_workgroups(p.H_kv), p.H_kv, 1);
-  hipLaunchKernelGGL((mixed_attention_kernel<D>), grid, dim3(kMixedWaves * kWave), 0, stream, p);
+  hipLaunchKernelGGL((mixed_attention_kernel<D>), grid, dim3(mixed_waves<D>() * kWave), 0, stream, p);
   return (int)hipGetLastError();
 }
 
@@ -474,7 +533,7 @@ extern "C" int64_t cie_mixed_partials_bytes(int64_t total_T, int64_t H_q, int64_
 
 extern "C" int64_t cie_mixed_counters(int64_t B, int64_t H_kv, int64_t max_seqlen) {
   if (B < 0 || H_kv <= 0 || max_seqlen < 0) return -1;
-  return B * H_kv * ((max_seqlen + 15) / 16);
+  return B * H_kv * ((max_seqlen + 15) / 16) * kMaxColGroups;
 }
 
 extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, const void* v_pool,
@@ -494,9 +553,12 @@ extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, c
     return CIE_EINVAL;
   const int64_t G = H_q / H_kv;
   const int64_t n_qtiles = (max_seqlen + 15) / 16;
+  // item indices (<= total_T tiles x groups x chunks) and a tile's partial
+  // region (16 * H_q rows of kMaxChunks * D floats) must fit in 31 bits
   if (G > 8 || page_size % 16 != 0 || B > kMaxSeqs || H_kv > 65535 ||
-      n_qtiles * kMaxChunks > 0x7fffffff || bt_width * page_size > 0x7fffffff ||
-      total_T > 0x7fffffff)
+      n_qtiles > 0x7fffffff || bt_width * page_size > 0x7fffffff ||
+      total_T * kMaxColGroups * kMaxChunks > 0x7fffffff ||
+      16 * H_q * kMaxChunks * D * 4 > 0x7fffffff)
     return CIE_EUNSUPPORTED;
   if (D != 64 && D != 128) return CIE_EUNSUPPORTED;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(o) |

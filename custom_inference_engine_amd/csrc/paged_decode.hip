@@ -317,7 +317,6 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   SoftmaxAcc<D, 1> st;
   st.init();
   const int lim[1] = {L};
-  constexpr int kNoKey = 0x3fffffff;  // key base of an absent second tile: masked everywhere
   for (int c0 = 0; c0 < n_mine; c0 += kWave) {
     // this chunk's page ids: lanes k = c0 + lane (the first chunk's first
     // kSpecTiles are already in flight)

@@ -57,7 +57,7 @@ def test_workspace_sizes(native_lib):
     assert native_lib.cie_paged_decode_max_splits() >= 16
     assert native_lib.cie_mixed_partials_bytes(1052, 14, 64) >= 1052 * 14 * 16 * 66 * 4
     assert native_lib.cie_mixed_partials_bytes(10, 0, 64) == -1
-    assert native_lib.cie_mixed_counters(32, 2, 256) == 32 * 2 * 16
+    assert native_lib.cie_mixed_counters(32, 2, 256) >= 32 * 2 * 16
 
 
 def _decode_args(**over):

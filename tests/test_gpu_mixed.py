@@ -59,6 +59,57 @@ def test_mixed_shapes(native_lib, prior, new):
     _check(case, o, f"mixed {prior}/{new}")
 
 
+@pytest.mark.parametrize("prior,new,d", [
+    ([16000, 5], [20, 1], 64),       # a prefix long enough to split over several workgroups
+    ([5000, 3000], [1, 33], 128),
+], ids=lambda x: str(x))
+def test_mixed_long_prefixes_split_keys(native_lib, prior, new, d):
+    case = inputs.make_case(prior, new, seed=37, d=d)
+    note(f"mixed long prefixes prior={prior} new={new} D={d}")
+    kp, vp, o = gpu_mixed_step(case)
+    _check(case, o, f"long {prior}/{new} D={d}")
+
+
+def test_mixed_partials_above_2gib_in_the_low_address_word(native_lib):
+    """Split tiles store partials through buffer descriptors built from the region's address.
+
+    The partials are placed where every address's low 32-bit word has bit 31
+    set; a descriptor that sign-extended that word into the high one would
+    point outside the allocation.
+    """
+    case = inputs.make_case([3071, 6000, 0], [1, 20, 5], seed=38)
+    note("mixed partials at a high low-word address")
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    lib = _native.load()
+    H_q, D = 14, 64
+    need = lib.cie_mixed_partials_bytes(case.T, H_q, D)
+    big = torch.empty(2**31 + 2 * need + 4096, dtype=torch.uint8, device=DEV)
+    base = big.data_ptr()
+    low = base % 2**32
+    if 2**31 <= low and low + need < 2**32:
+        off = 0
+    else:
+        off = (2**31 - low) % 2**32
+    off = (off + 255) // 256 * 256
+    ptr = base + off
+    assert 2**31 <= ptr % 2**32 and ptr % 2**32 + need < 2**32 and off + need <= big.numel()
+    o = torch.empty_like(c.q)
+    ctr = torch.zeros(lib.cie_mixed_counters(case.B, 2, 20), dtype=torch.int32, device=DEV)
+    rc = lib.cie_mixed_attention(o.data_ptr(), c.q.data_ptr(), kp.data_ptr(), vp.data_ptr(),
+                                 c.cu_seqlens.data_ptr(), c.kv_lens.data_ptr(), c.slot_ids.data_ptr(),
+                                 c.block_table.data_ptr(), ptr, ctr.data_ptr(), case.B, case.T,
+                                 20, H_q, 2, D,
+                                 16, kp.shape[0], kp.stride(0), kp.stride(1), c.block_table.stride(0),
+                                 c.block_table.shape[1], c.block_table.shape[0], None,
+                                 _native.stream_handle(torch.device(DEV)))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(ctr) == 0
+    del big
+    _check(case, o[0].float().cpu(), "partials at a high low-word address")
+
+
 def test_mixed_single_rows_match_decode_kernel(native_lib):
     """L = 1 sequences through the mixed kernel equal the decode kernel on the same pool."""
     case = inputs.make_case([0, 31, 512, 3071], seed=32)
@@ -119,7 +170,7 @@ def test_mixed_counters_return_to_zero(native_lib):
     c = case.to(DEV)
     kp, vp = (t.to(DEV) for t in case.appended_pools())
     from custom_inference_engine_amd import mixed_gqa_attention
-    ctr = torch.zeros(case.B * 2 * 3, dtype=torch.int32, device=DEV)
+    ctr = torch.zeros(_native.load().cie_mixed_counters(case.B, 2, 40), dtype=torch.int32, device=DEV)
     for _ in range(2):
         o = mixed_gqa_attention(c.q, kp, vp, 40, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
                                 counters=ctr)
