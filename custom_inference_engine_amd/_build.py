@@ -31,6 +31,9 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # no kernel produces NaN (masked scores are -inf, and -inf - -inf is
+    # guarded): lets max trees use v_max3 without canonicalizing moves
+    "-fno-honor-nans",
     "-munsafe-fp-atomics",
 ]
 

@@ -70,37 +70,86 @@ __device__ __forceinline__ TileLoc tile_loc(const int64_t* __restrict__ bt_row, 
   return TileLoc{page * page_stride + head_off + (int64_t)off * D};
 }
 
+// Loads of a step's two tiles.  Both tiles are always loaded (a caller with
+// only one tile passes it twice and masks the copy with key kNoKey), so every
+// step issues the same loads and the compiler can wait for exactly the
+// oldest step in flight instead of draining all loads.
 template <int D>
 __device__ __forceinline__ void load_pair(KVPair<D>& kv, const f16* __restrict__ kpool,
                                           const f16* __restrict__ vpool, TileLoc t0,
-                                          TileLoc t1, bool two, int r16, int grp) {
+                                          TileLoc t1, int r16, int grp) {
   constexpr int KS = Geo<D>::KS;
   constexpr int NT = Geo<D>::NT;
   typedef typename HVec<NT>::type vrow_t;
   const f16* k0 = kpool + t0.base + r16 * D + 8 * grp;
   const f16* v0 = vpool + t0.base + (4 * grp) * D + NT * r16;
+  const f16* k1 = kpool + t1.base + r16 * D + 8 * grp;
+  const f16* v1 = vpool + t1.base + (4 * grp) * D + NT * r16;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) kv.k[0][ks] = *reinterpret_cast<const f16x8*>(k0 + 32 * ks);
 #pragma unroll
   for (int e = 0; e < 4; ++e) kv.v[e] = *reinterpret_cast<const vrow_t*>(v0 + e * D);
-  if (two) {
-    const f16* k1 = kpool + t1.base + r16 * D + 8 * grp;
-    const f16* v1 = vpool + t1.base + (4 * grp) * D + NT * r16;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kv.k[1][ks] = *reinterpret_cast<const f16x8*>(k1 + 32 * ks);
+  for (int ks = 0; ks < KS; ++ks) kv.k[1][ks] = *reinterpret_cast<const f16x8*>(k1 + 32 * ks);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) kv.v[4 + e] = *reinterpret_cast<const vrow_t*>(v1 + e * D);
-  } else {
+  for (int e = 0; e < 4; ++e) kv.v[4 + e] = *reinterpret_cast<const vrow_t*>(v1 + e * D);
+}
+
+// A 16-key tile as a raw buffer: descriptor base = the tile's first row
+// (page, head and in-page offset applied; built with scalar ops from
+// wave-uniform values), num_records = its valid rows.  Loads past the valid
+// rows return 0 without touching memory, so rows at or past a sequence's end
+// read as zeros (the reference's masked loads) and an absent tile (0 rows)
+// costs no memory traffic.  The descriptor is per tile, so pools of any size
+// are addressed with 32-bit in-tile offsets.
+// All arguments must be wave-uniform (they are pinned to scalar registers
+// here so the descriptor never needs a per-lane loop).
+template <int D>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const f16* pool, int64_t elem_off,
+                                                           int valid_rows) {
+  const uint64_t a = reinterpret_cast<uint64_t>(pool + elem_off);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const int bytes = __builtin_amdgcn_readfirstlane(valid_rows * D * (int)sizeof(f16));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
+                                           bytes, kBufRsrcWord3);
+}
+
+// Per-lane byte offsets inside a tile of the K and V operands (loop
+// invariants): K[key r16][8*grp + 32*ks ..] and V[key 4*grp + e][NT*r16 ..].
+template <int D>
+struct TileLaneOffsets {
+  uint32_t k, v;
+  __device__ __forceinline__ TileLaneOffsets(int r16, int grp)
+      : k((uint32_t)((r16 * D + 8 * grp) * sizeof(f16))),
+        v((uint32_t)((4 * grp * D + Geo<D>::NT * r16) * sizeof(f16))) {}
+};
+
+template <int D>
+__device__ __forceinline__ void load_tile_buf(f16x8 (&k)[Geo<D>::KS],
+                                              typename HVec<Geo<D>::NT>::type (&v)[4],
+                                              __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                              const TileLaneOffsets<D>& lo) {
+  constexpr int KS = Geo<D>::KS;
+  constexpr int NT = Geo<D>::NT;
+  typedef typename HVec<NT>::type vrow_t;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kv.k[1][ks] = f16x8{};
+  for (int ks = 0; ks < KS; ++ks)
+    k[ks] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, lo.k + 64 * ks, 0, 0));
 #pragma unroll
-    for (int e = 0; e < 4; ++e) kv.v[4 + e] = vrow_t{};
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (NT == 4)
+      v[e] = __builtin_bit_cast(vrow_t, __builtin_amdgcn_raw_buffer_load_b64(rv, lo.v + e * D * 2, 0, 0));
+    else
+      v[e] = __builtin_bit_cast(vrow_t, __builtin_amdgcn_raw_buffer_load_b128(rv, lo.v + e * D * 2, 0, 0));
   }
 }
 
 // Zero the V rows at keys >= key_end (the masked loads of the reference read
 // 0 there; pool memory past a sequence's end may hold anything).  key0a /
-// key0b: first key of the pair's two tiles.
+// key0b: first key of the pair's two tiles (kNoKey: a masked copy).  A step
+// whose keys all lie below key_end needs no zeroing: a masked copy of a valid
+// tile holds finite values and gets probability 0.
 template <int D>
 __device__ __forceinline__ void zero_tail_rows(KVPair<D>& kv, int key0a, int key0b, int key_end,
                                                int grp) {
@@ -115,20 +164,27 @@ __device__ __forceinline__ void zero_tail_rows(KVPair<D>& kv, int key0a, int key
 // Online-softmax state for NCT 16-wide column tiles held by one wave.
 template <int D, int NCT>
 struct SoftmaxAcc {
-  float m[NCT];  // running max (log2 domain), identical across a column's 4 lanes
-  float l[NCT];  // lane-partial running sum (reduced over the 4 lanes at the end)
+  float m[NCT];     // reference max (log2 domain), identical across a column's 4 lanes
+  f32x4 lsum[NCT];  // [0]: the column's sum of P (an MFMA against ones: no lane reduction)
   f32x4 acc[NCT][Geo<D>::NT];
 
   __device__ __forceinline__ void init() {
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {
       m[c] = kNegInf;
-      l[c] = 0.f;
+      lsum[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int nt = 0; nt < Geo<D>::NT; ++nt) acc[c][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
+  __device__ __forceinline__ float l(int c) const { return lsum[c][0]; }
 };
+
+// The reference max of a column moves only when a step's max exceeds it by
+// more than kRescaleSlack (log2 units), so P = 2^(s - m) stays <= 2^slack
+// (exact in fp16, far from overflow in fp32) and the accumulator rescale is
+// rare.  o = acc / l does not depend on which reference max is used.
+constexpr float kRescaleSlack = 8.f;
 
 // One 32-key step for NCT column tiles.  key0a / key0b = absolute index of the
 // first key of the pair's two tiles (the tiles need not be adjacent; an absent
@@ -138,12 +194,12 @@ struct SoftmaxAcc {
 // skip the masking.
 //
 // The column tiles go in batches of up to kAttendBatch; a batch runs in
-// phases — its Q.K^T MFMAs, its columns' softmax updates, one (rare) rescale,
-// its P.V MFMAs — with no branch inside a phase, so one wave overlaps a column
-// tile's softmax with the MFMAs of the others.  VALU per column tile: the max
-// runs on raw scores (the scale is positive), exp2 takes fma(s, scale, -m),
-// and the accumulator rescale is skipped when no column's max moved
-// (alpha == 1 exactly).
+// phases — its Q.K^T MFMAs, its columns' maxima, one (rare) reference-max
+// update with accumulator rescale, its exponentials, its P.V MFMAs and the
+// P.1 MFMA that accumulates the row sums — with no branch inside a phase, so
+// one wave overlaps a column tile's VALU work with the MFMAs of the others.
+// The max runs on raw scores (the scale is positive) and exp2 takes
+// fma(s, scale, -m).
 #ifndef CIE_ATTEND_BATCH
 #define CIE_ATTEND_BATCH 4
 #endif
@@ -162,6 +218,7 @@ __device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const K
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int e = 0; e < 8; ++e) va[nt][e] = kv.v[e][nt];
+  const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
 
 #pragma unroll
   for (int c0 = 0; c0 < NCT; c0 += SB) {
@@ -178,61 +235,67 @@ __device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const K
         }
       }
     }
-    f16x8 pop[SB];
-    float alpha[SB];
-    bool moved = false;
+    float sc[SB][8];
+    float mb[SB];
+    bool need = false;
 #pragma unroll
     for (int i = 0; i < SB; ++i) {
       if (c0 + i < NCT) {
         const int c = c0 + i;
-        float sc[8];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          sc[r] = s[i][0][r];
-          sc[4 + r] = s[i][1][r];
+          sc[i][r] = s[i][0][r];
+          sc[i][4 + r] = s[i][1][r];
         }
         if constexpr (MASK) {
           const int kba = key0a + 4 * grp;
           const int kbb = key0b + 4 * grp;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            sc[r] = kba + r < lim[c] ? sc[r] : kNegInf;
-            sc[4 + r] = kbb + r < lim[c] ? sc[4 + r] : kNegInf;
+            sc[i][r] = kba + r < lim[c] ? sc[i][r] : kNegInf;
+            sc[i][4 + r] = kbb + r < lim[c] ? sc[i][4 + r] : kNegInf;
           }
         }
-        float mb = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
-                         fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-        mb = col_max4(mb) * scale_log2;
-        const float m_new = fmaxf(st.m[c], mb);
-        // A column with every key masked so far keeps m = -inf, l = 0,
-        // acc = 0; m_use keeps exp2 away from (-inf) - (-inf).
-        const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-        alpha[i] = fast_exp2(st.m[c] - m_use);
-        moved |= alpha[i] != 1.f;
-        float ps = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pe = fast_exp2(__builtin_fmaf(sc[e], scale_log2, -m_use));
-          ps += pe;
-          pop[i][e] = (f16)pe;
-        }
-        st.l[c] = __builtin_fmaf(st.l[c], alpha[i], ps);
-        st.m[c] = m_new;
+        const float x = fmaxf(fmaxf(fmaxf(sc[i][0], sc[i][1]), fmaxf(sc[i][2], sc[i][3])),
+                              fmaxf(fmaxf(sc[i][4], sc[i][5]), fmaxf(sc[i][6], sc[i][7])));
+        mb[i] = col_max4(x) * scale_log2;
+        need |= mb[i] > st.m[c] + kRescaleSlack;
       }
     }
-    if (__any(moved)) {
+    if (__any(need)) {  // rare: move the reference max, rescale the state
 #pragma unroll
-      for (int i = 0; i < SB; ++i)
-        if (c0 + i < NCT)
+      for (int i = 0; i < SB; ++i) {
+        if (c0 + i < NCT) {
+          const int c = c0 + i;
+          const float m_new = fmaxf(st.m[c], mb[i]);
+          // A column with every key masked so far keeps m = -inf, l = 0, acc = 0.
+          const float alpha = fast_exp2(st.m[c] - (m_new == kNegInf ? 0.f : m_new));
+          st.m[c] = m_new;
+          st.lsum[c][0] *= alpha;
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) st.acc[c0 + i][nt] *= alpha[i];
+          for (int nt = 0; nt < NT; ++nt) st.acc[c][nt] *= alpha;
+        }
+      }
+    }
+    f16x8 pop[SB];
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      if (c0 + i < NCT) {
+        const float m_use = st.m[c0 + i] == kNegInf ? 0.f : st.m[c0 + i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          pop[i][e] = (f16)fast_exp2(__builtin_fmaf(sc[i][e], scale_log2, -m_use));
+      }
     }
 #pragma unroll
-    for (int i = 0; i < SB; ++i)
-      if (c0 + i < NCT)
+    for (int i = 0; i < SB; ++i) {
+      if (c0 + i < NCT) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
           st.acc[c0 + i][nt] = mfma16x16x32(va[nt], pop[i], st.acc[c0 + i][nt]);
+        st.lsum[c0 + i] = mfma16x16x32(ones, pop[i], st.lsum[c0 + i]);
+      }
+    }
   }
 }
 
@@ -269,6 +332,8 @@ struct PagedSrc {
 // tiles per step.  The page ids of up to 64 tiles are gathered first, one per
 // lane, so a step's K/V loads depend on no other load; a ring of PF + 1
 // register-staged steps keeps PF steps of loads in flight ahead of the math.
+// Tiles are read through per-tile buffer descriptors (tile_rsrc), so keys at
+// or past key_end read as zeros.
 // key_end = number of keys that exist (rows at or past it are zeroed).
 template <int D, int NCT, int PF>
 __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
@@ -284,6 +349,7 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
   for (int off = 1; off < kWave; off <<= 1) mask_from = min(mask_from, __shfl_xor(mask_from, off, kWave));
   const int lane = threadIdx.x & (kWave - 1);
   const int tpp = src.page_size >> 4;  // 16-key tiles per page
+  const TileLaneOffsets<D> lanes(r16, grp);
   for (int c0 = t_begin; c0 < t_end; c0 += kWave) {
     const int n_chunk = min(kWave, t_end - c0);
     int page = 0;
@@ -298,32 +364,40 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
     const int n_pairs = (n_chunk + 1) >> 1;
     KVPair<D> ring[PF + 1];
     int keya[PF + 1], keyb[PF + 1];
+    // Every iteration issues one step's loads (past the last step: tiles
+    // with no valid rows, which read zeros and touch no memory), so the wait
+    // before a step's math covers that step's loads only.
     auto issue = [&](int slot, int j) {
+      const bool real = j < n_pairs;
+      j = min(j, n_pairs - 1);
       const int ka = 2 * j;  // chunk-local index of the step's first tile
       const bool two = ka + 1 < n_chunk;
       const int ta = c0 + ka;
+      const int tb = two ? ta + 1 : ta;
       const int pa = __builtin_amdgcn_readlane(page, ka);
       const int pb = two ? __builtin_amdgcn_readlane(page, ka + 1) : pa;
-      const TileLoc l0{(int64_t)pa * src.page_stride + src.head_off + (int64_t)((ta % tpp) * 16) * D};
-      const TileLoc l1{(int64_t)pb * src.page_stride + src.head_off +
-                       (int64_t)(((ta + 1) % tpp) * 16) * D};
-      keya[slot] = ta * 16;
-      keyb[slot] = two ? ta * 16 + 16 : kNoKey;
-      load_pair<D>(ring[slot], src.k_pool, src.v_pool, l0, l1, two, r16, grp);
+      const int key0a = ta * 16;
+      const int rows_a = real ? min(16, max(0, key_end - key0a)) : 0;
+      const int rows_b = (real && two) ? min(16, max(0, key_end - key0a - 16)) : 0;
+      const int64_t oa = (int64_t)pa * src.page_stride + src.head_off + (int64_t)((ta % tpp) * 16) * D;
+      const int64_t ob = (int64_t)pb * src.page_stride + src.head_off + (int64_t)((tb % tpp) * 16) * D;
+      typedef typename HVec<Geo<D>::NT>::type vrow_t;
+      typedef vrow_t vquad_t[4];
+      load_tile_buf<D>(ring[slot].k[0], *reinterpret_cast<vquad_t*>(&ring[slot].v[0]),
+                       tile_rsrc<D>(src.k_pool, oa, rows_a), tile_rsrc<D>(src.v_pool, oa, rows_a), lanes);
+      load_tile_buf<D>(ring[slot].k[1], *reinterpret_cast<vquad_t*>(&ring[slot].v[4]),
+                       tile_rsrc<D>(src.k_pool, ob, rows_b), tile_rsrc<D>(src.v_pool, ob, rows_b), lanes);
+      keya[slot] = key0a;
+      keyb[slot] = two ? key0a + 16 : kNoKey;
     };
 #pragma unroll
-    for (int j = 0; j < PF; ++j)
-      if (j < n_pairs) issue(j, j);
+    for (int j = 0; j < PF; ++j) issue(j, j);
     for (int j0 = 0; j0 < n_pairs; j0 += PF + 1) {
 #pragma unroll
       for (int u = 0; u <= PF; ++u) {
         const int j = j0 + u;
-        if (j < n_pairs) {
-          if (j + PF < n_pairs) issue((u + PF) % (PF + 1), j + PF);
-          const int ka = keya[u], kb = keyb[u];
-          if ((kb == kNoKey ? ka : kb) + 16 > key_end) zero_tail_rows<D>(ring[u], ka, kb, key_end, grp);
-          attend_pair<D, NCT>(st, ring[u], qop, ka, kb, lim, mask_from, scale_log2, grp);
-        }
+        issue((u + PF) % (PF + 1), j + PF);
+        if (j < n_pairs) attend_pair<D, NCT>(st, ring[u], qop, keya[u], keyb[u], lim, mask_from, scale_log2, grp);
       }
     }
   }

@@ -38,13 +38,13 @@ namespace cie {
 //   CIE_MIXED_PF           32-key steps of loads in flight per wave (D = 64)
 //   CIE_MIXED_WG_PER_CU    workgroups per CU in the grid
 #ifndef CIE_MIXED_WAVES
-#define CIE_MIXED_WAVES 8
+#define CIE_MIXED_WAVES 4
 #endif
 #ifndef CIE_MIXED_CG
-#define CIE_MIXED_CG 2
+#define CIE_MIXED_CG 4
 #endif
 #ifndef CIE_MIXED_WAVE_PAIRS
-#define CIE_MIXED_WAVE_PAIRS 10
+#define CIE_MIXED_WAVE_PAIRS 24
 #endif
 #ifndef CIE_MIXED_PF
 #define CIE_MIXED_PF 2
@@ -241,7 +241,7 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
   const PartRegion pr = part_region<D>(p, s, tp);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
-    const float l = col_sum4(st.l[c]);
+    const float l = st.l(c);
     __syncthreads();  // the previous column tile's fold has read the LDS
     if (grp == 0) {
       sm_m[wave][r16] = st.m[c];
@@ -422,8 +422,17 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
 // sequence item counts and their prefix sums in LDS — and takes items
 // blockIdx.x, blockIdx.x + gridDim.x, ...  (items ordered by sequence, tile,
 // column group, chunk), so no workgroup is launched for an empty slot.
+// Waves per SIMD the registers must allow: two when a wave carries at most
+// two column tiles (D = 64), else one.
 template <int D>
-__global__ __launch_bounds__(mixed_waves<D>() * kWave) void mixed_attention_kernel(MixedParams p) {
+constexpr int mixed_waves_per_simd() {
+  return D <= 64 && col_group<D>() <= 2 ? 2 : 1;
+}
+
+template <int D>
+__global__ __launch_bounds__(mixed_waves<D>() * kWave)
+__attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_attention_kernel(
+    MixedParams p) {
   static_assert(col_group<D>() <= 4 && 8 / col_group<D>() <= kMaxColGroups, "column groups");
   constexpr int W = mixed_waves<D>();
   constexpr int NTH = W * kWave;
@@ -462,7 +471,9 @@ __global__ __launch_bounds__(mixed_waves<D>() * kWave) void mixed_attention_kern
   }
   if (threadIdx.x == 0) sm_prefix[0] = 0;
   __syncthreads();
-  const int total = sm_prefix[p.B];
+  // (LDS reads look per-lane to the compiler: the plan's values are pinned
+  // to scalar registers, so everything derived from them stays scalar)
+  const int total = uniform(sm_prefix[p.B]);
   MIXED_TRACE(blockIdx.x, 6, __builtin_amdgcn_s_memrealtime());  // planning done (first item slot)
 
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
@@ -471,12 +482,12 @@ __global__ __launch_bounds__(mixed_waves<D>() * kWave) void mixed_attention_kern
     int lo = 0, hi = p.B;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (sm_prefix[mid] <= item) lo = mid;
+      if (uniform(sm_prefix[mid]) <= item) lo = mid;
       else hi = mid;
     }
-    const int b = lo;
+    const int b = uniform(lo);
     const SeqInfo s = seq_info(p, b);
-    int j = item - sm_prefix[b];
+    int j = item - uniform(sm_prefix[b]);
     int qt = 0;
     for (;; ++qt) {
       const TilePlan tp = tile_plan(qt, s, p.G, CG, W);
@@ -486,7 +497,7 @@ __global__ __launch_bounds__(mixed_waves<D>() * kWave) void mixed_attention_kern
     }
     MIXED_TRACE(item, 1, __builtin_amdgcn_s_memrealtime());
     MIXED_TRACE(item, 7, (uint64_t)(b * 1000 + qt));
-    process_item<D>(p, s, b, g, qt, j, sm_m, sm_l, sm_acc, &sm_last, item);
+    process_item<D>(p, s, b, g, uniform(qt), uniform(j), sm_m, sm_l, sm_acc, &sm_last, item);
   }
 }
 

@@ -126,25 +126,19 @@ __device__ __forceinline__ void load_tile_new(f16x8 (&k)[Geo<D>::KS],
   }
 }
 
+// Both tiles are always loaded (a step with one tile loads it twice and
+// masks the copy, key0b = kNoKey), as load_pair does.
 template <int D, bool kAppend>
 __device__ __forceinline__ void load_pair_new(KVPair<D>& kv, const PagedSrc& src, TileLoc t0,
-                                              TileLoc t1, bool two, int key0a, int key0b,
+                                              TileLoc t1, int key0a, int key0b,
                                               const NewRow<D>& nr, int r16, int grp) {
   typedef typename HVec<Geo<D>::NT>::type vrow_t;
   typedef vrow_t vquad_t[4];
   if constexpr (!kAppend) {
-    load_pair<D>(kv, src.k_pool, src.v_pool, t0, t1, two, r16, grp);
+    load_pair<D>(kv, src.k_pool, src.v_pool, t0, t1, r16, grp);
   } else {
     load_tile_new<D>(kv.k[0], *reinterpret_cast<vquad_t*>(&kv.v[0]), src, t0, key0a, nr, r16, grp);
-    if (two) {
-      load_tile_new<D>(kv.k[1], *reinterpret_cast<vquad_t*>(&kv.v[4]), src, t1, key0b, nr, r16,
-                       grp);
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < Geo<D>::KS; ++ks) kv.k[1][ks] = f16x8{};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) kv.v[4 + e] = vrow_t{};
-    }
+    load_tile_new<D>(kv.k[1], *reinterpret_cast<vquad_t*>(&kv.v[4]), src, t1, key0b, nr, r16, grp);
   }
 }
 
@@ -328,15 +322,19 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
     const int n_pairs = (n_chunk + 1) >> 1;
     // Ring of kPF + 1 register-staged pairs: pair j's loads are issued kPF
     // steps before its math, so up to kPF pairs of loads are in flight.
+    // Every iteration issues exactly one pair (past the end: the last pair
+    // again, a cache hit), so the wait before a pair's math covers that
+    // pair's loads only.
     constexpr int kPF = CIE_DECODE_PF;
     KVPair<D> ring[kPF + 1];
     TileLoc loc[kPF + 1][2];
     int keya[kPF + 1], keyb[kPF + 1];
     auto issue = [&](int slot_i, int j) {
+      j = min(j, n_pairs - 1);
       const int ka = 2 * j;                // chunk-local index of tile A
       const bool two = ka + 1 < n_chunk;
       const int ta = gw + (c0 + ka) * TW;  // tile ids
-      const int tb = ta + TW;
+      const int tb = two ? ta + TW : ta;
       const int pa = __builtin_amdgcn_readlane(pages, ka);
       const int pb = two ? __builtin_amdgcn_readlane(pages, ka + 1) : pa;
       loc[slot_i][0] = TileLoc{(int64_t)pa * src.page_stride + src.head_off +
@@ -345,18 +343,17 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
                                (int64_t)((tb % tpp) * 16) * D};
       keya[slot_i] = ta * 16;
       keyb[slot_i] = two ? tb * 16 : kNoKey;
-      load_pair_new<D, kAppend>(ring[slot_i], src, loc[slot_i][0], loc[slot_i][1], two,
-                                keya[slot_i], keyb[slot_i], nr, r16, grp);
+      load_pair_new<D, kAppend>(ring[slot_i], src, loc[slot_i][0], loc[slot_i][1], keya[slot_i],
+                                keyb[slot_i], nr, r16, grp);
     };
 #pragma unroll
-    for (int j = 0; j < kPF; ++j)
-      if (j < n_pairs) issue(j, j);
+    for (int j = 0; j < kPF; ++j) issue(j, j);
     for (int j0 = 0; j0 < n_pairs; j0 += kPF + 1) {
 #pragma unroll
       for (int u = 0; u <= kPF; ++u) {
         const int j = j0 + u;
+        issue((u + kPF) % (kPF + 1), j + kPF);
         if (j < n_pairs) {
-          if (j + kPF < n_pairs) issue((u + kPF) % (kPF + 1), j + kPF);
           KVPair<D>& cur = ring[u];
           const int ka = keya[u], kb = keyb[u];
           const int last_key = (kb == kNoKey ? ka : kb) + 16;
@@ -375,10 +372,9 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
 
   DECODE_TRACE(2, __builtin_amdgcn_s_memrealtime());
   // Fold the waves of this workgroup.
-  st.l[0] = col_sum4(st.l[0]);
   if (grp == 0) {
     sm_m[wave][r16] = st.m[0];
-    sm_l[wave][r16] = st.l[0];
+    sm_l[wave][r16] = st.l(0);
   }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)

@@ -165,7 +165,7 @@ def test_mixed_rows_beyond_max_seqlen_are_flagged(native_lib):
 
 def test_mixed_counters_return_to_zero(native_lib):
     """Multi-chunk tiles (long prefixes) leave their arrival counters zero."""
-    case = inputs.make_case([3000, 0, 2500, 700], [40, 1, 1, 18], seed=36)
+    case = inputs.make_case([6000, 0, 2500, 700], [40, 1, 1, 18], seed=36)
     note("mixed counters")
     c = case.to(DEV)
     kp, vp = (t.to(DEV) for t in case.appended_pools())
