@@ -34,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "paged GQA decode µs/call + HBM GB/s (% of peak) at B=32 kv_len=4096"
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 HBM_PEAK_GBPS = 8000.0
 MIN_ROTATION_BYTES = 512 << 20
 
@@ -329,7 +330,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel<64,4,append> (fused append + split-KV + merge, 1 launch/call)",
+            "kernel": "decode_kernel<64,8,true> (fused append + split-KV + merge, 1 launch/call)",
             "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
@@ -393,6 +394,10 @@ def bench_mixed(args, cie, inputs, ref, dev):
         "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
         "config": {"workload": "config 3 mixed: 4x256-row prefill chunks + 28 decode rows", "T": case.T,
                    "algorithmic_bytes": nbytes, "flops": flops, "layer_rotation": R},
+        "roofline": {"bound": "mfma", "kernel": "mixed_attention_kernel<64> (+ kv_append_kernel<8,false>)",
+                     "achieved": round(flops / (us * 1e-6) / 1e12, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                     "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None},
         "parity_max_abs_err": err,
     }), flush=True)
 
