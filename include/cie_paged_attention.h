@@ -158,8 +158,9 @@ int cie_paged_decode_append(void* o, const void* q, void* k_pool, void* v_pool,
  *                aligned, any contents (per-chunk softmax state)
  *   counters   : cie_mixed_counters(B, H_kv, max_seqlen) int32, 16-byte
  *                aligned, zero before the call and left zero by it (one
- *                arrival counter per query tile; the same buffer can serve
- *                cie_paged_decode, calls being stream-ordered)
+ *                arrival counter per query tile and column group; the same
+ *                buffer can serve cie_paged_decode, calls being
+ *                stream-ordered)
  */
 int64_t cie_mixed_partials_bytes(int64_t total_T, int64_t H_q, int64_t D);
 int64_t cie_mixed_counters(int64_t B, int64_t H_kv, int64_t max_seqlen);
