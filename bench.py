@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import statistics
@@ -44,7 +45,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=800, help="decode calls timed (rounded up to a multiple of R)")
     ap.add_argument("--warmup", type=int, default=80)
-    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4))
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5))
     ap.add_argument("--splits", type=int, default=None, help="KV splits (default: the library's policy)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of graph replay")
@@ -213,6 +214,8 @@ def main():
     torch.cuda.set_device(dev)
     if args.config == 3:
         return bench_mixed(args, cie, inputs, ref, dev)
+    if args.config == 5:
+        return bench_model(args, cie, dev)
     case = inputs.config2(seed=0) if args.config == 2 else inputs.config4(seed=0)
     splits = args.splits or (case.meta.get("n_splits") if args.config == 4 else None)
     log(f"config {args.config}: B={case.B} attend={int(case.attended[0])} pool pages={case.k_pool.shape[0]}")
@@ -400,6 +403,114 @@ def bench_mixed(args, cie, inputs, ref, dev):
                      "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None},
         "parity_max_abs_err": err,
     }), flush=True)
+
+
+def bench_model(args, cie, dev, batch: int = 32, new_tokens: int = 128, budget: int = 512,
+                sigma: float = 0.5):
+    """Config 5: a 24-layer Qwen2.5-0.5B-shaped model (random fp16 weights) through the drop-in.
+
+    B requests (prompt lengths lognormal, median 256, sigma recorded, clipped
+    to [16, 2048]) are prefilled by MixedModule in steps of at most `budget`
+    tokens (chunked prefill), then decoded for `new_tokens` steps by
+    DecodeModule (one hipGraph replay per step: every layer's fused append +
+    paged decode).  Reported: decode tokens/s and step time, graph replay
+    alone, the attention launches of one step alone, prefill tokens/s.
+    """
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    from custom_inference_engine_amd.scheduler import DecodeModule, MixedModule, assign_pages
+
+    cfg = Qwen2Config(hidden_size=896, num_attention_heads=14, num_key_value_heads=2, intermediate_size=4864,
+                      num_hidden_layers=24, vocab_size=151936, max_position_embeddings=32768, rope_theta=1e6,
+                      rms_norm_eps=1e-6, tie_word_embeddings=True)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Qwen2ForCausalLM(cfg)
+    model = model.half().eval()
+    cie.use_triton_attention(model)
+    kv = cie.KVStorage(cfg, max_cache_len=32768, page_size=16, n_slots=batch + 1, device=dev,
+                       dtype=torch.float16)
+    log(f"config 5: 24 layers, B={batch}, pool {kv.n_pages} pages; capturing the decode step graph")
+    dec = DecodeModule(model, kv, batch_size=batch)
+    mix = MixedModule(model, kv, token_count=budget)
+
+    g = torch.Generator().manual_seed(5)
+    lens = torch.exp(torch.randn(batch, generator=g) * sigma + math.log(256)).round().clamp(16, 2048).long()
+    prompts = [torch.randint(0, cfg.vocab_size, (int(n),), generator=g).tolist() for n in lens]
+    slots = list(range(1, batch + 1))
+    free = (torch.randperm(kv.n_pages - 1, generator=g) + 1).tolist()
+    extra = 64  # decode tokens beyond new_tokens (the replay-only timing)
+    for sl, p in zip(slots, prompts):
+        assign_pages(kv, sl, len(p) + new_tokens + extra, free)
+
+    # chunked prefill: each step packs up to `budget` tokens of the pending prompts
+    done = [0] * batch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n_steps = 0
+    while any(d < len(p) for d, p in zip(done, prompts)):
+        chunk, chunk_slots, left = [], [], budget
+        for i, p in enumerate(prompts):
+            if done[i] < len(p) and left > 0:
+                n = min(len(p) - done[i], left)
+                chunk.append(p[done[i]:done[i] + n])
+                chunk_slots.append(slots[i])
+                done[i] += n
+                left -= n
+        mix.forward(chunk, chunk_slots)
+        n_steps += 1
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    n_prompt = int(lens.sum())
+    log(f"prefill: {n_prompt} tokens in {n_steps} steps, {prefill_s * 1e3:.1f} ms")
+
+    # decode: full step (upload + replay + argmax + host sync), as the reference's DecodeModule.forward
+    for _ in range(3):
+        dec.forward(slots)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(new_tokens - 3):
+        dec.forward(slots)
+    torch.cuda.synchronize()
+    step_us = (time.perf_counter() - t0) / (new_tokens - 3) * 1e6
+    # graph replay alone
+    n_rep = extra - 8
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.inference_mode():
+        start.record()
+        for _ in range(n_rep):
+            dec.graph.replay()
+        end.record()
+    torch.cuda.synchronize()
+    replay_us = start.elapsed_time(end) * 1e3 / n_rep
+    # the attention launches of one step alone: 24 fused append + decode calls on the live pools
+    with torch.inference_mode():
+        q = torch.randn(1, batch, 14, 64, device=dev, dtype=torch.float16)
+        kn = torch.randn(1, batch, 2, 64, device=dev, dtype=torch.float16)
+    slot_t = torch.tensor(slots, device=dev)
+
+    def attn_step():
+        for layer in range(cfg.num_hidden_layers):
+            cie.decode_append_gqa_attention(q, kv.keys[layer], kv.values[layer], kn, kn, kv.lens, slot_t,
+                                            kv.block_table)
+    with torch.inference_mode():  # the step modules made the RNG's graph state an inference tensor
+        attn_us, _ = time_calls([attn_step], 40, 8, True, 3)
+    ctx = float((kv.lens[slots].float().mean()).item())
+    line = {
+        "metric": "config 5 decode tokens/s (24-layer Qwen2.5-0.5B shape, B=32, hipGraph decode step)",
+        "value": round(batch / (step_us * 1e-6), 1), "unit": "tokens/s", "higher_is_better": True,
+        "n_gpus": 1, "steps": new_tokens, "ms_per_step": round(step_us / 1e3, 4),
+        "decode_step_us": round(step_us, 1), "graph_replay_us": round(replay_us, 1),
+        "attention_us_per_step": round(attn_us, 1),
+        "attention_share_of_replay": round(attn_us / replay_us, 3),
+        "prefill_tokens_per_s": round(n_prompt / prefill_s, 1),
+        "dtype": "fp16 (fp32 accumulate)", "data": "synthetic (random weights, random prompt ids)",
+        "config": {"workload": "Qwen2.5-0.5B-shaped forward, random init from a local Qwen2Config",
+                   "layers": 24, "batch": batch, "prompt_len_median": 256, "prompt_len_sigma": sigma,
+                   "prompt_tokens": n_prompt, "new_tokens": new_tokens, "token_budget": budget,
+                   "prefill_steps": n_steps, "pool_tokens": 32768, "mean_context_at_end": round(ctx, 1)},
+    }
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

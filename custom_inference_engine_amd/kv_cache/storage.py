@@ -179,13 +179,16 @@ class KVStorage:
             slot_ids, self.lens, self.block_table,
         )
 
+    # lens[unused_idx] = 0 as a device kernel (a 1-element multiply), not a
+    # host scalar copy, so a decode step that contains it can be graph-captured
+    # (and no memset node lands in the graph).
     def decode_advance(self, slot_ids: torch.Tensor) -> None:
         self.lens[slot_ids] += 1
-        self.lens[self.unused_idx] = 0
+        self.lens[self.unused_idx:self.unused_idx + 1].mul_(0)
 
     def mixed_advance(self, slot_ids: torch.Tensor, lens: torch.Tensor) -> None:
         self.lens[slot_ids] += lens
-        self.lens[self.unused_idx] = 0
+        self.lens[self.unused_idx:self.unused_idx + 1].mul_(0)
 
     def reset(self, slot_ids: list[int]) -> None:
         self.lens[slot_ids] = 0

@@ -1,0 +1,12 @@
+"""Step modules around the attention path, mirroring the reference's scheduler/ layout.
+
+``DecodeModule`` (scheduler/decode_module.py:8-107 of the reference) captures a
+whole decode step of the model — every layer's fused KV append + paged decode —
+in one hipGraph per batch bucket and replays it; ``MixedModule``
+(scheduler/mixed_module.py:10-133) runs a packed chunked-prefill / decode
+step eagerly.  The scheduling policy itself (token budget, admission,
+preemption) is not part of this package.
+"""
+from .decode_module import DecodeModule  # noqa: F401
+from .mixed_module import MixedModule  # noqa: F401
+from .slots import assign_pages, pad_slot_ids  # noqa: F401
