@@ -301,7 +301,8 @@ def main():
     wl = ("paged GQA decode call = KV append + split-KV load + merge, one layer, one launch" if args.config == 2
           else "long-context paged GQA decode call (config 4)")
     line = {
-        "metric": METRIC,
+        "metric": METRIC if args.config == 2 else
+        "long-context paged GQA decode us/call + HBM GB/s (% of peak) at B=16 kv_len=16384 (config 4)",
         "value": round(gbps, 1),
         "unit": "GB/s",
         "n_gpus": 1,

@@ -201,13 +201,30 @@ constexpr float kRescaleSlack = 8.f;
 // The max runs on raw scores (the scale is positive) and exp2 takes
 // fma(s, scale, -m).
 #ifndef CIE_ATTEND_BATCH
-#define CIE_ATTEND_BATCH 4
+#define CIE_ATTEND_BATCH 2
 #endif
 constexpr int kAttendBatch = CIE_ATTEND_BATCH;
 
-template <int D, int NCT, bool MASK>
+// Where a step reads the Q^T operands of its column tiles: registers
+// (QRegs) or this wave's LDS block (QLds: one 16-byte slot per (column tile,
+// k-step, lane), so a read is one conflict-free ds_read_b128).
+template <int D, int NCT>
+struct QRegs {
+  const f16x8 (&q)[NCT][Geo<D>::KS];
+  __device__ __forceinline__ f16x8 operator()(int c, int ks) const { return q[c][ks]; }
+};
+template <int D>
+struct QLds {
+  const f16x8* base;  // [column tile][k-step][lane]
+  int lane;
+  __device__ __forceinline__ f16x8 operator()(int c, int ks) const {
+    return base[(c * Geo<D>::KS + ks) * kWave + lane];
+  }
+};
+
+template <int D, int NCT, bool MASK, class QS>
 __device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const KVPair<D>& kv,
-                                                 const f16x8 (&qop)[NCT][Geo<D>::KS], int key0a,
+                                                 const QS& qop, int key0a,
                                                  int key0b, const int (&lim)[NCT],
                                                  float scale_log2, int grp) {
   constexpr int KS = Geo<D>::KS;
@@ -230,8 +247,9 @@ __device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const K
         s[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          s[i][0] = mfma16x16x32(kv.k[0][ks], qop[c0 + i][ks], s[i][0]);
-          s[i][1] = mfma16x16x32(kv.k[1][ks], qop[c0 + i][ks], s[i][1]);
+          const f16x8 qk = qop(c0 + i, ks);
+          s[i][0] = mfma16x16x32(kv.k[0][ks], qk, s[i][0]);
+          s[i][1] = mfma16x16x32(kv.k[1][ks], qk, s[i][1]);
         }
       }
     }
@@ -299,15 +317,15 @@ __device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const K
   }
 }
 
-template <int D, int NCT>
+template <int D, int NCT, class QS>
 __device__ __forceinline__ void attend_pair(SoftmaxAcc<D, NCT>& st, const KVPair<D>& kv,
-                                            const f16x8 (&qop)[NCT][Geo<D>::KS], int key0a,
+                                            const QS& qop, int key0a,
                                             int key0b, const int (&lim)[NCT], int mask_from,
                                             float scale_log2, int grp) {
   if (max(key0a, key0b) + 16 > mask_from)  // uniform
-    attend_pair_body<D, NCT, true>(st, kv, qop, key0a, key0b, lim, scale_log2, grp);
+    attend_pair_body<D, NCT, true, QS>(st, kv, qop, key0a, key0b, lim, scale_log2, grp);
   else
-    attend_pair_body<D, NCT, false>(st, kv, qop, key0a, key0b, lim, scale_log2, grp);
+    attend_pair_body<D, NCT, false, QS>(st, kv, qop, key0a, key0b, lim, scale_log2, grp);
 }
 
 // Output dim held by (grp, r, nt) of the P.V accumulator.
@@ -335,9 +353,8 @@ struct PagedSrc {
 // Tiles are read through per-tile buffer descriptors (tile_rsrc), so keys at
 // or past key_end read as zeros.
 // key_end = number of keys that exist (rows at or past it are zeroed).
-template <int D, int NCT, int PF>
-__device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
-                                             const f16x8 (&qop)[NCT][Geo<D>::KS],
+template <int D, int NCT, int PF, class QS>
+__device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& qop,
                                              const int (&lim)[NCT], int t_begin, int t_end,
                                              int key_end, const PagedSrc& src, float scale_log2,
                                              int r16, int grp) {
@@ -397,7 +414,8 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st,
       for (int u = 0; u <= PF; ++u) {
         const int j = j0 + u;
         issue((u + PF) % (PF + 1), j + PF);
-        if (j < n_pairs) attend_pair<D, NCT>(st, ring[u], qop, keya[u], keyb[u], lim, mask_from, scale_log2, grp);
+        if (j < n_pairs)
+          attend_pair<D, NCT, QS>(st, ring[u], qop, keya[u], keyb[u], lim, mask_from, scale_log2, grp);
       }
     }
   }

@@ -36,6 +36,8 @@ namespace cie {
 //   CIE_MIXED_WAVE_PAIRS   32-key steps per wave before a tile's keys are
 //                          split over several workgroups
 //   CIE_MIXED_PF           32-key steps of loads in flight per wave (D = 64)
+//   CIE_MIXED_QLDS         1: the item's Q operands live in LDS, not registers
+//                          (a wave then fits 256 registers at D = 64)
 //   CIE_MIXED_WG_PER_CU    workgroups per CU in the grid
 #ifndef CIE_MIXED_WAVES
 #define CIE_MIXED_WAVES 4
@@ -47,7 +49,10 @@ namespace cie {
 #define CIE_MIXED_WAVE_PAIRS 24
 #endif
 #ifndef CIE_MIXED_PF
-#define CIE_MIXED_PF 2
+#define CIE_MIXED_PF 1
+#endif
+#ifndef CIE_MIXED_QLDS
+#define CIE_MIXED_QLDS 1
 #endif
 #ifndef CIE_MIXED_WG_PER_CU
 #define CIE_MIXED_WG_PER_CU 1
@@ -224,18 +229,31 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
                                           const TilePlan& tp, int g, int ct0, int chunk, int w0,
                                           int w1, const PagedSrc& src, int wave, int r16, int grp,
                                           float (*sm_m)[16], float (*sm_l)[16],
-                                          float (*sm_acc)[16][D + 4], int item) {
+                                          float (*sm_acc)[16][D + 4], f16x8* sm_q, int item) {
   constexpr int NT = Geo<D>::NT;
+  constexpr int KS = Geo<D>::KS;
   constexpr int W = mixed_waves<D>();
-  f16x8 qop[NCT][Geo<D>::KS];
+  f16x8 qop[NCT][KS];
   int lim[NCT];
 #pragma unroll
   for (int c = 0; c < NCT; ++c) load_combo_q<D>(p, s, tp, g, ct0 + c, r16, grp, qop[c], lim[c]);
   MIXED_TRACE(item, 9, __builtin_amdgcn_s_memrealtime());
   SoftmaxAcc<D, NCT> st;
   st.init();
-  stream_tiles<D, NCT, mixed_pf<D>()>(st, qop, lim, w0, w1, tp.key_end, src, p.scale_log2, r16,
-                                      grp);
+  if constexpr (CIE_MIXED_QLDS) {
+    // this wave's block of Q operands in LDS (read back by this wave only)
+    f16x8* mine = sm_q + wave * (col_group<D>() * KS * kWave);
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) mine[(c * KS + ks) * kWave + lane] = qop[c][ks];
+    stream_tiles<D, NCT, mixed_pf<D>()>(st, QLds<D>{mine, lane}, lim, w0, w1, tp.key_end, src,
+                                        p.scale_log2, r16, grp);
+  } else {
+    stream_tiles<D, NCT, mixed_pf<D>()>(st, QRegs<D, NCT>{qop}, lim, w0, w1, tp.key_end, src,
+                                        p.scale_log2, r16, grp);
+  }
   MIXED_TRACE(item, 8, __builtin_amdgcn_s_memrealtime());
   const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
   const PartRegion pr = part_region<D>(p, s, tp);
@@ -365,7 +383,8 @@ __device__ __forceinline__ int seq_items(const SeqInfo& s, int n_qtiles, int G, 
 template <int D>
 __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo& s, int b, int g,
                                              int qt, int j, float (*sm_m)[16], float (*sm_l)[16],
-                                             float (*sm_acc)[16][D + 4], int* sm_last, int item) {
+                                             float (*sm_acc)[16][D + 4], f16x8* sm_q, int* sm_last,
+                                             int item) {
   constexpr int CG = col_group<D>();
   constexpr int W = mixed_waves<D>();
   const int lane = threadIdx.x & (kWave - 1);
@@ -389,7 +408,7 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   case k:                                                                                      \
     if constexpr (k <= CG)                                                                     \
       run_group<D, k>(p, s, tp, g, ct0, chunk, w0, w1, src, wave, r16, grp, sm_m, sm_l, sm_acc, \
-                      item);                                                                   \
+                      sm_q, item);                                                             \
     break;
     CIE_GROUP_CASE(1)
     CIE_GROUP_CASE(2)
@@ -423,10 +442,10 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
 // blockIdx.x, blockIdx.x + gridDim.x, ...  (items ordered by sequence, tile,
 // column group, chunk), so no workgroup is launched for an empty slot.
 // Waves per SIMD the registers must allow: two when a wave carries at most
-// two column tiles (D = 64), else one.
+// two column tiles or keeps its Q operands in LDS (D = 64), else one.
 template <int D>
 constexpr int mixed_waves_per_simd() {
-  return D <= 64 && col_group<D>() <= 2 ? 2 : 1;
+  return D <= 64 && (col_group<D>() <= 2 || CIE_MIXED_QLDS) ? 2 : 1;
 }
 
 template <int D>
@@ -439,6 +458,7 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
   __shared__ float sm_m[W][16];
   __shared__ float sm_l[W][16];
   __shared__ __attribute__((aligned(16))) float sm_acc[W][16][D + 4];
+  __shared__ f16x8 sm_q[CIE_MIXED_QLDS ? W * col_group<D>() * Geo<D>::KS * kWave : 1];
   __shared__ int sm_last;
   __shared__ int sm_prefix[kMaxSeqs + 1];
   __shared__ int sm_scan[NTH];
@@ -497,7 +517,7 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     }
     MIXED_TRACE(item, 1, __builtin_amdgcn_s_memrealtime());
     MIXED_TRACE(item, 7, (uint64_t)(b * 1000 + qt));
-    process_item<D>(p, s, b, g, uniform(qt), uniform(j), sm_m, sm_l, sm_acc, &sm_last, item);
+    process_item<D>(p, s, b, g, uniform(qt), uniform(j), sm_m, sm_l, sm_acc, sm_q, &sm_last, item);
   }
 }
 

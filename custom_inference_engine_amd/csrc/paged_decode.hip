@@ -364,7 +364,7 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
               if (pos >= ka) store_new_row<D>(cur, src, loc[u][0], loc[u][1], ka, kb, pos, r16, grp);
             }
           }
-          attend_pair<D, 1>(st, cur, qop, ka, kb, lim, L, p.scale_log2, grp);
+          attend_pair<D, 1>(st, cur, QRegs<D, 1>{qop}, ka, kb, lim, L, p.scale_log2, grp);
         }
       }
     }
