@@ -36,6 +36,12 @@ sys.path.insert(0, ROOT)
 
 METRIC = "paged GQA decode µs/call + HBM GB/s (% of peak) at B=32 kv_len=4096"
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+# HBM bytes per launch of the measured kernel, from rocprofv3 FETCH_SIZE x 2.0 +
+# WRITE_SIZE (scale factors from a plain 256 MiB copy), committed under profiles/
+TRAFFIC_BYTES = {
+    2: (69_727_027, "profiles/hbm_traffic_decode_config2.md"),
+    3: (48_401_203, "profiles/mixed_attention_config3.md"),
+}
 HBM_PEAK_GBPS = 8000.0
 MIN_ROTATION_BYTES = 512 << 20
 
@@ -341,7 +347,8 @@ def main():
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
             "us_per_launch": round(us_call, 3),
             "algorithmic_bytes_per_launch": bytes_call,
-            "traffic": None,
+            "traffic": TRAFFIC_BYTES.get(args.config, (None, None))[0],
+            "traffic_source": TRAFFIC_BYTES.get(args.config, (None, None))[1],
         },
         "paged_gather_ceiling": {
             "what": "probe kernel reading the call's byte volume as shuffled 2 KiB chunks (no math)",
@@ -401,7 +408,8 @@ def bench_mixed(args, cie, inputs, ref, dev):
         "roofline": {"bound": "mfma", "kernel": "mixed_attention_kernel<64> (+ kv_append_kernel<8,false>)",
                      "achieved": round(flops / (us * 1e-6) / 1e12, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                     "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "traffic": TRAFFIC_BYTES[3][0], "traffic_source": TRAFFIC_BYTES[3][1]},
         "parity_max_abs_err": err,
     }), flush=True)
 
