@@ -191,11 +191,10 @@ __device__ __forceinline__ float partial_load(const float* ptr) {
 #endif
 }
 
-constexpr int kMaxSplits = 64;  // LDS staging bound of the merge (G <= 16)
+constexpr int kMaxSplits = 64;
 
 template <int D, int NTHREADS>
-__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g, float* sm_ms,
-                                             float* sm_ls);
+__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g);
 
 // Profiling builds only (-DCIE_DECODE_TRACE): wave 0 of every workgroup
 // stamps phase boundaries (s_memrealtime) into the buffer passed as `err`.
@@ -437,38 +436,57 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   if (!sm_last) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #endif
-  // the fold's LDS is free again: reuse it to stage the splits' m / l
-  merge_splits<D, WAVES * kWave>(p, b, g, &sm_acc[0][0][0], &sm_acc[0][0][0] + 16 * kMaxSplits);
+  merge_splits<D, WAVES * kWave>(p, b, g);
   if (threadIdx.x == 0) p.counters[b * p.H_kv + g] = 0;
   DECODE_TRACE(4, __builtin_amdgcn_s_memrealtime());
 #endif
 }
 
-// Combine the S partial states of every head of (b, g) into o.  The m / l of
-// all splits are staged in LDS first (scratch of >= G * S floats each).
+// Combine the S partial states of every head of (b, g) into o.  A thread
+// owns one (head, d) and takes the splits in groups of kMergeGroup: the m, l
+// and acc loads of a group are all issued before any is used (one memory round
+// trip per group), and a running log-sum-exp carries across groups.  For
+// S <= kMergeGroup the arithmetic is the plain max-then-sum of
+// kernels/decode_attention.py:243-264.
+constexpr int kMergeGroup = 8;
+
 template <int D, int NTHREADS>
-__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g, float* sm_ms,
-                                             float* sm_ls) {
+__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g) {
   const int S = p.n_splits;
   const int64_t row0 = ((int64_t)b * p.H_q + g * p.G) * S;
-  __syncthreads();
-  for (int i = threadIdx.x; i < p.G * S; i += NTHREADS) {
-    sm_ms[i] = partial_load(&p.part_m[row0 + i]);
-    sm_ls[i] = partial_load(&p.part_l[row0 + i]);
-  }
-  __syncthreads();
   for (int it = threadIdx.x; it < p.G * D; it += NTHREADS) {
     const int h = it / D;
     const int d = it - h * D;
-    float M = kNegInf;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, sm_ms[h * S + s]);
-    float num = 0.f, den = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < S; ++s) {
-      const float ms = sm_ms[h * S + s];
-      const float a = ms == kNegInf ? 0.f : fast_exp2(ms - M);
-      num += a * partial_load(&p.part_acc[(row0 + h * S + s) * D + d]);
-      den += a * sm_ls[h * S + s];
+    const int64_t r0 = row0 + (int64_t)h * S;
+    float M = kNegInf, num = 0.f, den = 0.f;
+    for (int s0 = 0; s0 < S; s0 += kMergeGroup) {
+      float ms[kMergeGroup], ls[kMergeGroup], as[kMergeGroup];
+#pragma unroll
+      for (int u = 0; u < kMergeGroup; ++u) {
+        ms[u] = kNegInf;
+        ls[u] = 0.f;
+        as[u] = 0.f;
+        if (s0 + u < S) {
+          ms[u] = partial_load(&p.part_m[r0 + s0 + u]);
+          ls[u] = partial_load(&p.part_l[r0 + s0 + u]);
+          as[u] = partial_load(&p.part_acc[(r0 + s0 + u) * D + d]);
+        }
+      }
+      float Mn = M;
+#pragma unroll
+      for (int u = 0; u < kMergeGroup; ++u) Mn = fmaxf(Mn, ms[u]);
+      if (Mn == kNegInf) continue;  // no split of this group saw a key
+      // rescale what earlier groups summed (exp2(-inf) = 0 while M is unset)
+      const float c = fast_exp2(M - Mn);
+      num *= c;
+      den *= c;
+#pragma unroll
+      for (int u = 0; u < kMergeGroup; ++u) {
+        const float a = ms[u] == kNegInf ? 0.f : fast_exp2(ms[u] - Mn);
+        num += a * as[u];
+        den += a * ls[u];
+      }
+      M = Mn;
     }
     p.o[((int64_t)b * p.H_q + g * p.G + h) * D + d] =
         (f16)((M == kNegInf || den == 0.f) ? 0.f : num / den);
@@ -478,9 +496,7 @@ __device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g
 // Separate merge launch (CIE_DECODE_MERGE == 3): one workgroup per (g, b).
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
-  __shared__ float sm_ms[16 * kMaxSplits];
-  __shared__ float sm_ls[16 * kMaxSplits];
-  merge_splits<D, 256>(p, blockIdx.y, blockIdx.x, sm_ms, sm_ls);
+  merge_splits<D, 256>(p, blockIdx.y, blockIdx.x);
 }
 
 // Waves per workgroup: D = 128 needs twice the registers, so half the waves.
