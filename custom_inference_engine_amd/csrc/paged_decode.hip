@@ -198,16 +198,25 @@ __device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g
 
 // Profiling builds only (-DCIE_DECODE_TRACE): wave 0 of every workgroup
 // stamps phase boundaries (s_memrealtime) into the buffer passed as `err`.
+// A stamp waits for nothing but its own clock read.
 #ifdef CIE_DECODE_TRACE
-#define DECODE_TRACE(k, v)                                                                \
+constexpr int kTraceSlots = 24;
+#define DECODE_TRACE_LANE0(k, v)                                                          \
   do {                                                                                    \
-    if (threadIdx.x == 0 && p.err != nullptr) {                                         \
-      __builtin_amdgcn_s_waitcnt(0);                                                      \
-      reinterpret_cast<uint64_t*>(p.err)[((int64_t)(b * p.H_kv + g) * p.n_splits + split) * 8 + \
+    if ((threadIdx.x & (kWave - 1)) == 0 && p.err != nullptr) {                         \
+      reinterpret_cast<uint64_t*>(p.err)[((int64_t)(b * p.H_kv + g) * p.n_splits + split) * \
+                                             kTraceSlots +                                \
                                          (k)] = (v);                                      \
     }                                                                                     \
   } while (0)
+#define DECODE_TRACE(k, v)                  \
+  do {                                      \
+    if (threadIdx.x < kWave) DECODE_TRACE_LANE0(k, v); \
+  } while (0)
 #else
+#define DECODE_TRACE_LANE0(k, v) \
+  do {                           \
+  } while (0)
 #define DECODE_TRACE(k, v) \
   do {                     \
   } while (0)
@@ -219,7 +228,8 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   constexpr int NT = Geo<D>::NT;
   __shared__ float sm_m[WAVES][16];
   __shared__ float sm_l[WAVES][16];
-  __shared__ float sm_acc[WAVES][16][D + 1];
+  // rows padded to keep 16-byte alignment for the vector reads of the fold
+  __shared__ f32x4 sm_acc[WAVES][16][D / 4 + 1];
   __shared__ int sm_last;
 
   const int split = blockIdx.x;
@@ -310,14 +320,48 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   SoftmaxAcc<D, 1> st;
   st.init();
   const int lim[1] = {L};
-  for (int c0 = 0; c0 < n_mine; c0 += kWave) {
+
+  // A wave with an odd tile count takes its last tile out of the two-tile
+  // steps: that tile's loads go out now, ahead of the first step's, and it is
+  // attended right after the first step (whose wait covers it: loads complete
+  // in issue order).  When the tiles of a (sequence, kv head) do not divide
+  // evenly over its waves, the waves holding one tile more would otherwise run
+  // one more dependent step than all the others, and every wave of the call
+  // would wait for them.  In append mode the new token's rows, if they sit in
+  // that tile, are stored to the pool after the loop: a store inside the loop
+  // would make every later wait there cover the store's completion too.
+  typedef typename HVec<NT>::type vrow_t;
+  typedef vrow_t vquad_t[4];
+  const bool odd = n_mine & 1;
+  const int n_main = n_mine - (odd ? 1 : 0);
+  KVPair<D> xt;
+  int xkey = kNoKey;
+  TileLoc xloc{0};
+  if (odd) {
+    const int kx = n_mine - 1;
+    const int tx = gw + kx * TW;
+    const int px = kx < kSpecTiles ? __builtin_amdgcn_readlane(pages, kx) : uniform(lane_page(kx));
+    xloc = TileLoc{(int64_t)px * src.page_stride + src.head_off + (int64_t)((tx % tpp) * 16) * D};
+    xkey = tx * 16;
+    load_tile_new<D>(xt.k[0], *reinterpret_cast<vquad_t*>(&xt.v[0]), src, xloc, xkey, nr, r16, grp);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) xt.k[1][ks] = f16x8{};
+#pragma unroll
+    for (int e = 4; e < 8; ++e) xt.v[e] = vrow_t{};
+  }
+  auto attend_odd = [&]() {
+    if (xkey + 16 >= L) zero_tail_rows<D>(xt, xkey, kNoKey, L, grp);
+    attend_pair<D, 1>(st, xt, QRegs<D, 1>{qop}, xkey, kNoKey, lim, L, p.scale_log2, grp);
+  };
+
+  for (int c0 = 0; c0 < n_main; c0 += kWave) {
     // this chunk's page ids: lanes k = c0 + lane (the first chunk's first
     // kSpecTiles are already in flight)
-    if (c0 > 0 || n_mine > kSpecTiles) {
+    if (c0 > 0 || n_main > kSpecTiles) {
       const int k = c0 + lane;
-      if (c0 > 0 || lane >= kSpecTiles) pages = k < n_mine ? lane_page(k) : 0;
+      if (c0 > 0 || lane >= kSpecTiles) pages = k < n_main ? lane_page(k) : 0;
     }
-    const int n_chunk = min(kWave, n_mine - c0);
+    const int n_chunk = min(kWave, n_main - c0);
     const int n_pairs = (n_chunk + 1) >> 1;
     // Ring of kPF + 1 register-staged pairs: pair j's loads are issued kPF
     // steps before its math, so up to kPF pairs of loads are in flight.
@@ -365,51 +409,73 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
           }
           attend_pair<D, 1>(st, cur, QRegs<D, 1>{qop}, ka, kb, lim, L, p.scale_log2, grp);
         }
+        if (odd && c0 == 0 && j == 0) attend_odd();
       }
+    }
+  }
+  if (odd) {
+    if (n_main == 0) attend_odd();
+    if constexpr (kAppend) {
+      if (pos >= xkey && pos < xkey + 16)
+        store_new_row<D>(xt, src, xloc, xloc, xkey, kNoKey, pos, r16, grp);
     }
   }
 
   DECODE_TRACE(2, __builtin_amdgcn_s_memrealtime());
-  // Fold the waves of this workgroup.
+  DECODE_TRACE_LANE0(16 + wave, __builtin_amdgcn_s_memrealtime());
+  // Fold the waves of this workgroup.  Lane (r16, grp) holds dims
+  // NT*(4*grp + r) + nt of column r16: for each r, NT consecutive dims, written
+  // as NT/4 16-byte vectors.  One thread then folds 4 dims of one head.
   if (grp == 0) {
     sm_m[wave][r16] = st.m[0];
     sm_l[wave][r16] = st.l(0);
   }
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
+  for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sm_acc[wave][r16][acc_dim<D>(grp, r, nt)] = st.acc[0][nt][r];
+    for (int n4 = 0; n4 < NT / 4; ++n4)
+      sm_acc[wave][r16][(NT * (4 * grp + r)) / 4 + n4] =
+          f32x4{st.acc[0][4 * n4][r], st.acc[0][4 * n4 + 1][r], st.acc[0][4 * n4 + 2][r],
+                st.acc[0][4 * n4 + 3][r]};
   __syncthreads();
+  DECODE_TRACE(8, __builtin_amdgcn_s_memrealtime());
 
-  for (int it = threadIdx.x; it < p.G * D; it += WAVES * kWave) {
-    const int h = it / D;
-    const int d = it - h * D;
+  constexpr int D4 = D / 4;
+  const int64_t row0 = ((int64_t)b * p.H_q + g * p.G) * S;  // partial row of (b, head g*G, split 0)
+  const __amdgpu_buffer_rsrc_t racc =
+      coherent_rsrc(p.part_acc + row0 * D, (uint32_t)(p.G * S * D * sizeof(float)));
+  for (int it = threadIdx.x; it < p.G * D4; it += WAVES * kWave) {
+    const int h = it / D4;
+    const int d4 = it - h * D4;
     float M = kNegInf;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][h]);
-    float num = 0.f, den = 0.f;
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
       const float mw = sm_m[w][h];
-      if (mw != kNegInf) {
-        const float a = fast_exp2(mw - M);
-        num += a * sm_acc[w][h][d];
-        den += a * sm_l[w][h];
-      }
+      // a wave that saw no key has m = -inf, l = 0, acc = 0
+      const float a = mw == kNegInf ? 0.f : fast_exp2(mw - M);
+      num += a * sm_acc[w][h][d4];
+      den += a * sm_l[w][h];
     }
     if (S == 1) {
-      p.o[((int64_t)b * p.H_q + g * p.G + h) * D + d] =
-          (f16)((M == kNegInf || den == 0.f) ? 0.f : num / den);
+      const bool none = M == kNegInf || den == 0.f;
+      f16x4 o4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o4[i] = (f16)(none ? 0.f : num[i] / den);
+      *reinterpret_cast<f16x4*>(p.o + ((int64_t)b * p.H_q + g * p.G + h) * D + 4 * d4) = o4;
     } else {
-      const int64_t row = ((int64_t)b * p.H_q + g * p.G + h) * S + split;
-      partial_store(&p.part_acc[row * D + d], num);
-      if (d == 0) {
-        partial_store(&p.part_m[row], M);
-        partial_store(&p.part_l[row], den);
+      const int row = h * S + split;  // within (b, g)
+      agent_store4(racc, (uint32_t)((row * D + 4 * d4) * sizeof(float)), num);
+      if (d4 == 0) {
+        partial_store(&p.part_m[row0 + row], M);
+        partial_store(&p.part_l[row0 + row], den);
       }
     }
   }
-  DECODE_TRACE(3, __builtin_amdgcn_s_memrealtime());
+  DECODE_TRACE(9, __builtin_amdgcn_s_memrealtime());
   if (S == 1) return;
 
 #if CIE_DECODE_MERGE != 3
@@ -419,11 +485,13 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   // (vmcnt 0) they are visible device-wide, so no L2 writeback is needed
   // before the arrival count.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // s_waitcnt vmcnt(0)
+  DECODE_TRACE(3, __builtin_amdgcn_s_memrealtime());
   __syncthreads();
   if (threadIdx.x == 0)
     sm_last = __hip_atomic_fetch_add(&p.counters[b * p.H_kv + g], 1, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT) == S - 1;
   __syncthreads();
+  DECODE_TRACE(10, __builtin_amdgcn_s_memrealtime());
   if (!sm_last) return;
 #else
   __syncthreads();
@@ -443,7 +511,7 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
 }
 
 // Combine the S partial states of every head of (b, g) into o.  A thread
-// owns one (head, d) and takes the splits in groups of kMergeGroup: the m, l
+// owns 4 dims of one head and takes the splits in groups of kMergeGroup: the m, l
 // and acc loads of a group are all issued before any is used (one memory round
 // trip per group), and a running log-sum-exp carries across groups.  For
 // S <= kMergeGroup the arithmetic is the plain max-then-sum of
@@ -452,24 +520,29 @@ constexpr int kMergeGroup = 8;
 
 template <int D, int NTHREADS>
 __device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g) {
+  constexpr int D4 = D / 4;
   const int S = p.n_splits;
   const int64_t row0 = ((int64_t)b * p.H_q + g * p.G) * S;
-  for (int it = threadIdx.x; it < p.G * D; it += NTHREADS) {
-    const int h = it / D;
-    const int d = it - h * D;
-    const int64_t r0 = row0 + (int64_t)h * S;
-    float M = kNegInf, num = 0.f, den = 0.f;
+  const __amdgpu_buffer_rsrc_t racc =
+      coherent_rsrc(p.part_acc + row0 * D, (uint32_t)(p.G * S * D * sizeof(float)));
+  for (int it = threadIdx.x; it < p.G * D4; it += NTHREADS) {
+    const int h = it / D4;
+    const int d4 = it - h * D4;
+    const int r0 = h * S;  // partial row of (h, split 0) within (b, g)
+    float M = kNegInf, den = 0.f;
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < S; s0 += kMergeGroup) {
-      float ms[kMergeGroup], ls[kMergeGroup], as[kMergeGroup];
+      float ms[kMergeGroup], ls[kMergeGroup];
+      f32x4 as[kMergeGroup];
 #pragma unroll
       for (int u = 0; u < kMergeGroup; ++u) {
         ms[u] = kNegInf;
         ls[u] = 0.f;
-        as[u] = 0.f;
+        as[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (s0 + u < S) {
-          ms[u] = partial_load(&p.part_m[r0 + s0 + u]);
-          ls[u] = partial_load(&p.part_l[r0 + s0 + u]);
-          as[u] = partial_load(&p.part_acc[(r0 + s0 + u) * D + d]);
+          ms[u] = partial_load(&p.part_m[row0 + r0 + s0 + u]);
+          ls[u] = partial_load(&p.part_l[row0 + r0 + s0 + u]);
+          as[u] = agent_load4(racc, (uint32_t)(((r0 + s0 + u) * D + 4 * d4) * sizeof(float)));
         }
       }
       float Mn = M;
@@ -488,8 +561,11 @@ __device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g
       }
       M = Mn;
     }
-    p.o[((int64_t)b * p.H_q + g * p.G + h) * D + d] =
-        (f16)((M == kNegInf || den == 0.f) ? 0.f : num / den);
+    const bool none = M == kNegInf || den == 0.f;
+    f16x4 o4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o4[i] = (f16)(none ? 0.f : num[i] / den);
+    *reinterpret_cast<f16x4*>(p.o + ((int64_t)b * p.H_q + g * p.G + h) * D + 4 * d4) = o4;
   }
 }
 
@@ -554,7 +630,8 @@ static int decode_entry(DecodeParams& p, void* partials, int32_t* counters, int6
       bt_width * page_size > 0x7fffffff)
     return CIE_EUNSUPPORTED;
   if (D != 64 && D != 128) return CIE_EUNSUPPORTED;
-  if ((reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k_pool) |
+  if ((reinterpret_cast<uintptr_t>(p.o) | reinterpret_cast<uintptr_t>(p.q) |
+       reinterpret_cast<uintptr_t>(p.k_pool) |
        reinterpret_cast<uintptr_t>(p.v_pool) | reinterpret_cast<uintptr_t>(partials) |
        reinterpret_cast<uintptr_t>(counters)) & 15)
     return CIE_EINVAL;

@@ -90,7 +90,7 @@ int cie_kv_append_tokens(void* k_pool, void* v_pool,
  * Replaces decode_gqa_attention (attn/core.py:13-66), i.e. the Triton
  * decode_gqa_attention_kernel_load (kernels/decode_attention.py:12-179) and
  * decode_attention_kernel_merge (kernels/decode_attention.py:182-272).
- *   q, o       : (B, H_q, D) dense fp16
+ *   q, o       : (B, H_q, D) dense fp16, 16-byte aligned
  *   lens       : (B,) attended lengths (the reference passes lens[slot] + 1)
  *   n_splits   : KV splits per (sequence, kv head) — the reference's
  *                `num_programs`

@@ -61,7 +61,7 @@ def test_workspace_sizes(native_lib):
 
 
 def _decode_args(**over):
-    a = dict(o=8, q=16, k=32, v=48, lens=64, slots=80, bt=96, ws=112, ctr=128, B=1, H_q=14, H_kv=2, D=64,
+    a = dict(o=144, q=16, k=32, v=48, lens=64, slots=80, bt=96, ws=112, ctr=128, B=1, H_q=14, H_kv=2, D=64,
              page_size=16, n_pages=64, page_stride=2048, head_stride=1024, bt_stride=64,
              bt_width=64, n_slots=2, n_splits=4)
     a.update(over)
@@ -84,6 +84,7 @@ def _call_decode(lib, a):
     ({"D": 96}, -2),                   # head_dim outside the built set
     ({"H_q": 34, "H_kv": 2}, -2),      # more than 16 query heads per kv head
     ({"q": 18}, -1),                   # q not 16-byte aligned
+    ({"o": 8}, -1),                    # o not 16-byte aligned
     ({"lens": 0}, -1),                 # null index pointer
     ({"ctr": 0}, -1),                  # split counters needed when n_splits > 1
     ({"n_splits": 65}, -2),            # above the merge's split limit
