@@ -11,11 +11,15 @@ from .attn.core import (  # noqa: F401
     GQA_PREFILL_CONFIG,
     HipQwen2Attention,
     TritonQwen2Attention,
+    append_tokens_qkv_rope,
     decode_append_gqa_attention,
     decode_gqa_attention,
+    decode_qkv_rope_gqa_attention,
     gqa_decode_append_attention_op,
     gqa_decode_attention_op,
+    gqa_decode_qkv_rope_attention_op,
     gqa_mixed_attention_op,
+    kv_append_tokens_qkv_rope_op,
     mixed_gqa_attention,
     replace_attention,
     use_triton_attention,

@@ -49,6 +49,17 @@ _SIGNATURES = {
          _c_i64p, _c_i64p, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
+    "cie_paged_decode_qkv_rope": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64p, _c_i64p, _c_i64p,
+         _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
+    "cie_kv_append_tokens_qkv_rope": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64p, _c_i64p, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
     "cie_mixed_partials_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "cie_mixed_counters": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "cie_mixed_attention": (
@@ -62,7 +73,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -20,7 +20,11 @@ capture they come from the graph pool), split partials likewise; the decode
 kernels' arrival counters are one persistent, self-cleaning buffer per device
 (``split_counters``).
 The decode op also has a fused form, ``inference::gqa_decode_append_attention``,
-that performs ``KVStorage.decode_update`` and the decode in one launch.
+that performs ``KVStorage.decode_update`` and the decode in one launch, and
+the drop-in goes one step further by default: from the fused QKV projection's
+output, ``inference::gqa_decode_qkv_rope_attention`` does the QKV split, RoPE,
+the append and the decode in one launch, and ``inference::kv_append_tokens_qkv_rope``
+does the split, RoPE and ``KVStorage.mixed_update`` of a mixed step in one.
 """
 from __future__ import annotations
 
@@ -199,6 +203,107 @@ def decode_append_gqa_attention(q, k_cache, v_cache, k, v, lens, slot_ids, block
     return o
 
 
+def _qkv_rows(qkv: torch.Tensor, width: int) -> torch.Tensor:
+    """(1, T, width) fused projection output -> (T, width) rows the kernels can read."""
+    _require(qkv.dim() == 3 and qkv.shape[0] == 1 and qkv.shape[2] == width,
+             f"qkv must be (1, T, {width})")
+    _require(qkv.dtype == torch.float16, "qkv must be float16")
+    rows = qkv[0]
+    if rows.stride(1) != 1 or rows.stride(0) % 8 or rows.data_ptr() % 16:
+        rows = rows.contiguous()
+    return rows
+
+
+def _rope_rows(t: torch.Tensor, n: int, d: int) -> torch.Tensor:
+    """cos / sin of shape (1, n, d) or (n, d) -> (n, d) rows, 16-byte aligned."""
+    _require(t.dtype == torch.float16, "cos / sin must be float16")
+    rows = t.reshape(-1, d)
+    _require(rows.shape[0] == n, "one cos / sin row per token")
+    if rows.stride(1) != 1 or rows.stride(0) % 8 or rows.data_ptr() % 16:
+        rows = rows.contiguous()
+    return rows
+
+
+def decode_qkv_rope_gqa_attention(qkv, cos, sin, k_cache, v_cache, lens, slot_ids, block_table,
+                                  num_heads: int, num_programs=None, err=None, counters=None):
+    """Decode step from the fused QKV projection output, one launch.
+
+    ``qkv`` (1, B, (H_q + 2·H_kv)·D) is ``F.linear(hidden, qkv_weight, qkv_bias)``
+    of TritonQwen2Attention (attn/core.py:181-184); ``cos`` / ``sin`` (1, B, D)
+    are the step's rotary tables.  Same result as splitting q / k / v,
+    ``apply_rotary_pos_emb`` (attn/core.py:193-198, computed in fp32 and
+    rounded once to fp16) and ``decode_append_gqa_attention``: the pools gain
+    the rotated k and v rows at ``lens[slot_ids[b]]``; returns o (1, B, H_q, D).
+    """
+    N_PAGES, H_kv, PAGE_SIZE, D = k_cache.shape
+    H_q = int(num_heads)
+    B = slot_ids.shape[0]
+    _require(H_q % H_kv == 0, "H_q must be a multiple of H_kv")
+    _require(N_PAGES == block_table.shape[1], "block_table width must equal n_pages")
+    rows = _qkv_rows(qkv, (H_q + 2 * H_kv) * D)
+    _require(rows.shape[0] == B, "decode takes one query token per sequence")
+    q_like = rows.new_empty((1, B, H_q, D))
+    _check_pool(q_like, k_cache, v_cache)
+    dev = _native.require_device(rows, cos, sin, k_cache, v_cache, lens, slot_ids, block_table)
+    cr, sr = _rope_rows(cos, B, D), _rope_rows(sin, B, D)
+    _require(cr.stride(0) == sr.stride(0), "cos and sin need the same row stride")
+    lens, slot_ids, block_table = _index(lens), _index(slot_ids), _block_table(block_table)
+    P = int(num_programs) if num_programs else default_decode_splits(B, H_kv, dev)
+    _require(P >= 1, "num_programs must be >= 1")
+
+    lib = _native.load()
+    o = q_like
+    if B == 0:
+        return o
+    _require(P <= lib.cie_paged_decode_max_splits(), "num_programs above the kernel's split limit")
+    partials, counters = _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters)
+    _native.check(
+        lib.cie_paged_decode_qkv_rope(
+            o.data_ptr(), rows.data_ptr(), rows.stride(0), cr.data_ptr(), sr.data_ptr(), cr.stride(0),
+            k_cache.data_ptr(), v_cache.data_ptr(), lens.data_ptr(), slot_ids.data_ptr(),
+            block_table.data_ptr(), partials.data_ptr(), counters.data_ptr(),
+            B, H_q, H_kv, D, PAGE_SIZE, N_PAGES, k_cache.stride(0), k_cache.stride(1),
+            block_table.stride(0), block_table.shape[1], lens.shape[0], P,
+            _native.ptr(err), _native.stream_handle(dev),
+        ),
+        "cie_paged_decode_qkv_rope",
+    )
+    return o
+
+
+def append_tokens_qkv_rope(qkv, cos, sin, k_cache, v_cache, pages, offsets, num_heads: int,
+                           err=None):
+    """Mixed-step QKV split + RoPE + ``KVStorage.mixed_update`` in one launch.
+
+    Token t of ``qkv`` (1, T, (H_q + 2·H_kv)·D) is rotated with ``cos`` /
+    ``sin`` row t; its k and v rows go to ``(pages[t], :, offsets[t])`` of the
+    pools (kv_cache/storage.py:62-85) and the rotated q is returned as
+    (1, T, H_q, D), ready for ``mixed_gqa_attention``.
+    """
+    N_PAGES, H_kv, PAGE_SIZE, D = k_cache.shape
+    H_q = int(num_heads)
+    rows = _qkv_rows(qkv, (H_q + 2 * H_kv) * D)
+    T = rows.shape[0]
+    q = rows.new_empty((1, T, H_q, D))
+    _check_pool(q, k_cache, v_cache)
+    _require(tuple(pages.shape) == (T,) and tuple(offsets.shape) == (T,), "pages / offsets must be (T,)")
+    dev = _native.require_device(rows, cos, sin, k_cache, v_cache, pages, offsets)
+    cr, sr = _rope_rows(cos, T, D), _rope_rows(sin, T, D)
+    _require(cr.stride(0) == sr.stride(0), "cos and sin need the same row stride")
+    pages, offsets = _index(pages), _index(offsets)
+    lib = _native.load()
+    _native.check(
+        lib.cie_kv_append_tokens_qkv_rope(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), rows.data_ptr(), rows.stride(0),
+            cr.data_ptr(), sr.data_ptr(), cr.stride(0), pages.data_ptr(), offsets.data_ptr(),
+            T, H_q, H_kv, PAGE_SIZE, D, N_PAGES, k_cache.stride(0), k_cache.stride(1),
+            _native.ptr(err), _native.stream_handle(dev),
+        ),
+        "cie_kv_append_tokens_qkv_rope",
+    )
+    return q
+
+
 def _as_rows(x: torch.Tensor, h_kv: int, d: int) -> torch.Tensor:
     try:
         rows = x.view(-1, h_kv, d)
@@ -286,6 +391,35 @@ def _(q, k_cache, v_cache, k, v, lens, slot_ids, block_table):
     return torch.empty_like(q)
 
 
+@torch.library.custom_op("inference::gqa_decode_qkv_rope_attention",
+                         mutates_args=("k_cache", "v_cache"))
+def gqa_decode_qkv_rope_attention_op(
+    qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor,
+    v_cache: torch.Tensor, lens: torch.Tensor, slot_ids: torch.Tensor, block_table: torch.Tensor,
+    num_heads: int,
+) -> torch.Tensor:
+    return decode_qkv_rope_gqa_attention(qkv, cos, sin, k_cache, v_cache, lens, slot_ids, block_table,
+                                         num_heads, **GQA_DECODE_CONFIG)
+
+
+@gqa_decode_qkv_rope_attention_op.register_fake
+def _(qkv, cos, sin, k_cache, v_cache, lens, slot_ids, block_table, num_heads):
+    return qkv.new_empty((1, qkv.shape[1], num_heads, k_cache.shape[-1]))
+
+
+@torch.library.custom_op("inference::kv_append_tokens_qkv_rope", mutates_args=("k_cache", "v_cache"))
+def kv_append_tokens_qkv_rope_op(
+    qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor,
+    v_cache: torch.Tensor, pages: torch.Tensor, offsets: torch.Tensor, num_heads: int,
+) -> torch.Tensor:
+    return append_tokens_qkv_rope(qkv, cos, sin, k_cache, v_cache, pages, offsets, num_heads)
+
+
+@kv_append_tokens_qkv_rope_op.register_fake
+def _(qkv, cos, sin, k_cache, v_cache, pages, offsets, num_heads):
+    return qkv.new_empty((1, qkv.shape[1], num_heads, k_cache.shape[-1]))
+
+
 @torch.library.custom_op("inference::gqa_mixed_attention", mutates_args=())
 def gqa_mixed_attention_op(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -307,7 +441,10 @@ class TritonQwen2Attention(torch.nn.Module):
 
     Fused QKV projection -> RoPE -> KV append (decode or token mode) -> paged
     attention (decode or mixed) -> o_proj.  Falls back to the wrapped HF module
-    when no ``kv_manager`` is passed.
+    when no ``kv_manager`` is passed.  By default the split, RoPE and append
+    run inside the HIP kernels (``fuse_rope``; a decode step is one launch);
+    ``fuse_rope = False`` / ``fuse_append = False`` select the reference's
+    sequence of separate calls.
     """
 
     def __init__(self, original_attn):
@@ -331,6 +468,11 @@ class TritonQwen2Attention(torch.nn.Module):
         # decode branch: KV append fused into the decode launch (one kernel)
         # instead of decode_update + gqa_decode_attention (two).
         self.fuse_append = True
+        # QKV split + RoPE fused into the append kernels (decode: into the
+        # decode launch; mixed: one append launch that also emits rotated q)
+        # instead of views, apply_rotary_pos_emb's elementwise kernels and the
+        # plain append.
+        self.fuse_rope = True
 
     def forward(self, hidden_states, position_embeddings, attention_mask=None,
                 past_key_values=None, kv_manager=None, **kwargs):
@@ -344,6 +486,28 @@ class TritonQwen2Attention(torch.nn.Module):
         attn = self.original
         total_T = hidden_states.shape[1]
         hidden_shape = (1, total_T, -1, self.head_dim)
+        keys, values = kv_manager.keys[self.layer_idx], kv_manager.values[self.layer_idx]
+        if self.fuse_qkv and self.fuse_rope and (self.fuse_append or not metadata.full_decode):
+            qkv = torch.nn.functional.linear(hidden_states, self.qkv_weight, self.qkv_bias)
+            cos, sin = position_embeddings
+            if metadata.full_decode:
+                o = gqa_decode_qkv_rope_attention_op(
+                    qkv, cos, sin, keys, values, kv_manager.lens, metadata.slot_ids,
+                    kv_manager.block_table, self.num_heads,
+                )
+            else:
+                query_states = kv_append_tokens_qkv_rope_op(
+                    qkv, cos, sin, keys, values, metadata.pages, metadata.offsets, self.num_heads,
+                )
+                o = gqa_mixed_attention_op(
+                    query_states, keys, values,
+                    kv_lens=kv_manager.lens[metadata.slot_ids], max_seqlen=metadata.max_seqlen,
+                    cu_seqlens=metadata.cu_seqlens, slot_ids=metadata.slot_ids,
+                    block_table=kv_manager.block_table,
+                )
+            attn_output = attn.o_proj(o.reshape(1, total_T, self.num_heads * self.head_dim))
+            return attn_output, None
+
         if self.fuse_qkv:
             q, k, v = torch.nn.functional.linear(hidden_states, self.qkv_weight, self.qkv_bias).split(
                 self.qkv_sizes, dim=-1)

@@ -62,6 +62,23 @@ __device__ __forceinline__ float col_sum4(float x) {
   return a + b;
 }
 
+// RoPE (transformers' apply_rotary_pos_emb: x*cos + rotate_half(x)*sin) of 8
+// dims i (lo) and their partners i + D/2 (hi): lo' = lo*c_lo - hi*s_lo,
+// hi' = hi*c_hi + lo*s_hi.  A product of two fp16 values is exact in fp32, so
+// each output is the exact two-term sum rounded once to fp32, then to fp16.
+__device__ __forceinline__ void rope8(f16x8& lo, f16x8& hi, f16x8 c_lo, f16x8 c_hi, f16x8 s_lo,
+                                      f16x8 s_hi) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float x0 = (float)lo[j];
+    const float x1 = (float)hi[j];
+    const float y0 = __builtin_fmaf(x0, (float)c_lo[j], -(x1 * (float)s_lo[j]));
+    const float y1 = __builtin_fmaf(x1, (float)c_hi[j], x0 * (float)s_hi[j]);
+    lo[j] = (f16)y0;
+    hi[j] = (f16)y1;
+  }
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

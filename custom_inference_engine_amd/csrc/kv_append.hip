@@ -87,6 +87,76 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   *reinterpret_cast<vec_t*>(p.v_pool + dst) = vv;
 }
 
+// Token mode from the fused QKV projection, with RoPE: row t of qkv holds
+// q (H_q heads), k (H_kv) and v (H_kv), D each.  A lane takes dims [8c, 8c+8)
+// and their rotate_half partners [8c + D/2, ...) of one (token, head): q heads
+// are rotated into q_out (T, H_q, D); kv heads have K rotated and V copied
+// into (pages[t], head, offsets[t]) of the pools.  This is the QKV split,
+// apply_rotary_pos_emb and KVStorage.mixed_update of TritonQwen2Attention's
+// mixed branch (attn/core.py:181-198, 226-229) in one launch.
+struct QkvRopeParams {
+  f16* q_out;
+  f16* k_pool;
+  f16* v_pool;
+  const f16* qkv;
+  const f16* cos;
+  const f16* sin;
+  const int64_t* pages;
+  const int64_t* offsets;
+  int64_t qkv_stride, cs_stride;
+  int64_t T, n_pages, pool_page_stride, pool_head_stride;
+  int32_t H_q, H_kv, page_size, D;
+  int32_t* err;
+};
+
+__global__ __launch_bounds__(256) void qkv_rope_append_kernel(QkvRopeParams p) {
+  const int halves = p.D / 16;  // lanes per (token, head)
+  const int heads = p.H_q + p.H_kv;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.T * heads * halves) return;
+  const int c = (int)(gid % halves);
+  const int h = (int)((gid / halves) % heads);
+  const int64_t t = gid / ((int64_t)halves * heads);
+  const int half = p.D / 2;
+  const int d0 = 8 * c;
+
+  const f16* crow = p.cos + t * p.cs_stride;
+  const f16* srow = p.sin + t * p.cs_stride;
+  const f16x8 c_lo = *reinterpret_cast<const f16x8*>(crow + d0);
+  const f16x8 c_hi = *reinterpret_cast<const f16x8*>(crow + d0 + half);
+  const f16x8 s_lo = *reinterpret_cast<const f16x8*>(srow + d0);
+  const f16x8 s_hi = *reinterpret_cast<const f16x8*>(srow + d0 + half);
+  const f16* x = p.qkv + t * p.qkv_stride + (int64_t)h * p.D;
+  f16x8 lo = *reinterpret_cast<const f16x8*>(x + d0);
+  f16x8 hi = *reinterpret_cast<const f16x8*>(x + d0 + half);
+  rope8(lo, hi, c_lo, c_hi, s_lo, s_hi);
+
+  if (h < p.H_q) {
+    f16* dst = p.q_out + (t * p.H_q + h) * p.D;
+    *reinterpret_cast<f16x8*>(dst + d0) = lo;
+    *reinterpret_cast<f16x8*>(dst + d0 + half) = hi;
+    return;
+  }
+  const int hk = h - p.H_q;
+  const int64_t page = p.pages[t];
+  const int64_t off = p.offsets[t];
+  if (off < 0 || off >= p.page_size) {
+    set_err(p.err, CIE_ERRBIT_OFFSET);
+    return;
+  }
+  if (page < 0 || page >= p.n_pages) {
+    set_err(p.err, CIE_ERRBIT_PAGE);
+    return;
+  }
+  const int64_t row = page * p.pool_page_stride + hk * p.pool_head_stride + off * p.D;
+  *reinterpret_cast<f16x8*>(p.k_pool + row + d0) = lo;
+  *reinterpret_cast<f16x8*>(p.k_pool + row + d0 + half) = hi;
+  const f16* v = x + (int64_t)p.H_kv * p.D;  // v block: H_kv heads after k
+  *reinterpret_cast<f16x8*>(p.v_pool + row + d0) = *reinterpret_cast<const f16x8*>(v + d0);
+  *reinterpret_cast<f16x8*>(p.v_pool + row + d0 + half) =
+      *reinterpret_cast<const f16x8*>(v + d0 + half);
+}
+
 static bool aligned16(const void* ptr) {
   return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0;
 }
@@ -191,4 +261,50 @@ extern "C" int cie_kv_append_tokens(
   p.D = (int32_t)D;
   p.err = err;
   return launch_append<false>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int cie_kv_append_tokens_qkv_rope(
+    void* q_out, void* k_pool, void* v_pool, const void* qkv, int64_t qkv_row_stride,
+    const void* cos, const void* sin, int64_t cs_row_stride, const int64_t* pages,
+    const int64_t* offsets, int64_t T, int64_t H_q, int64_t H_kv, int64_t page_size, int64_t D,
+    int64_t n_pages, int64_t pool_page_stride, int64_t pool_head_stride, int32_t* err,
+    void* stream) {
+  if (T < 0 || H_q <= 0 || H_kv <= 0 || page_size <= 0 || D <= 0 || n_pages <= 0)
+    return CIE_EINVAL;
+  if (D % 16 != 0 || H_q + H_kv > 0x7fffffff || page_size > 0x7fffffff || D > 0x7fffffff)
+    return CIE_EUNSUPPORTED;
+  if (T == 0) return CIE_OK;
+  if (!q_out || !k_pool || !v_pool || !qkv || !cos || !sin || !pages || !offsets)
+    return CIE_EINVAL;
+  if (!aligned16(q_out) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(qkv) ||
+      !aligned16(cos) || !aligned16(sin) || qkv_row_stride % 8 != 0 || cs_row_stride % 8 != 0 ||
+      pool_page_stride % 8 != 0 || pool_head_stride % 8 != 0 ||
+      qkv_row_stride < (H_q + 2 * H_kv) * D || cs_row_stride < D)
+    return CIE_EINVAL;
+  QkvRopeParams p{};
+  p.q_out = static_cast<f16*>(q_out);
+  p.k_pool = static_cast<f16*>(k_pool);
+  p.v_pool = static_cast<f16*>(v_pool);
+  p.qkv = static_cast<const f16*>(qkv);
+  p.cos = static_cast<const f16*>(cos);
+  p.sin = static_cast<const f16*>(sin);
+  p.pages = pages;
+  p.offsets = offsets;
+  p.qkv_stride = qkv_row_stride;
+  p.cs_stride = cs_row_stride;
+  p.T = T;
+  p.n_pages = n_pages;
+  p.pool_page_stride = pool_page_stride;
+  p.pool_head_stride = pool_head_stride;
+  p.H_q = (int32_t)H_q;
+  p.H_kv = (int32_t)H_kv;
+  p.page_size = (int32_t)page_size;
+  p.D = (int32_t)D;
+  p.err = err;
+  const int64_t total = T * (H_q + H_kv) * (D / 16);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffff) return CIE_EUNSUPPORTED;
+  hipLaunchKernelGGL(qkv_rope_append_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return (int)hipGetLastError();
 }

@@ -5,7 +5,7 @@
 // slot_ids[b]: o = softmax(q . K^T * D^-0.5) . V, o = 0 when L == 0 (the
 // -inf guard of kernels/decode_attention.py:260-264).
 //
-// Two entry modes share the kernel:
+// Three entry modes share the kernel:
 //  * plain  (cie_paged_decode): L = lens[b], the pool is read-only — the
 //    reference's gqa_decode_attention op.
 //  * append (cie_paged_decode_append): pos = lens_pool[slot], L = pos + 1; the
@@ -13,6 +13,11 @@
 //    exactly as KVStorage.decode_update (kv_cache/storage.py:87-122) does, and
 //    the wave that owns that tile reads them from k_new / v_new instead of the
 //    pool, so the append costs no extra launch and no extra round trip.
+//  * append + rope (cie_paged_decode_qkv_rope): q, k_new and v_new are column
+//    blocks of the fused QKV projection's output row, and q and k_new are
+//    rotated in registers (RoPE of transformers' apply_rotary_pos_emb, as
+//    TritonQwen2Attention.forward applies it, attn/core.py:193-198) before use;
+//    the pool receives the rotated K row.
 //
 // Work split.  Grid (n_splits, H_kv, B), WAVES wavefronts per workgroup.  The
 // reference interleaves 16-row blocks over its P programs
@@ -48,6 +53,10 @@ namespace cie {
 struct DecodeParams {
   f16* o;
   const f16* q;
+  int64_t q_row_stride;  // elements between sequences' q rows (H_q * D when dense)
+  const f16* cos;        // rope mode: (B, D) rows of the new token's cos / sin
+  const f16* sin;
+  int64_t cs_stride;
   f16* k_pool;
   f16* v_pool;
   const f16* k_new;  // append mode: (B, H_kv, D) rows with the strides below
@@ -65,37 +74,6 @@ struct DecodeParams {
   float scale_log2;
   int32_t* err;
 };
-
-// Attended length of sequence b (clamped to what its block-table row can
-// address; an invalid slot attends nothing) and, in append mode, the new
-// token's position (-1 when there is nothing to append).
-template <bool kAppend>
-__device__ __forceinline__ int decode_len(const DecodeParams& p, int b, int64_t& slot, int& pos) {
-  pos = -1;
-  slot = p.slot_ids[b];
-  if (slot < 0 || slot >= p.n_slots) {
-    set_err(p.err, CIE_ERRBIT_PAGE);
-    slot = 0;
-    return 0;
-  }
-  const int64_t cap = (int64_t)p.bt_width * p.page_size;
-  if constexpr (kAppend) {
-    const int64_t prior = p.lens[slot];
-    if (prior < 0 || prior + 1 > cap) {
-      set_err(p.err, CIE_ERRBIT_LEN);
-      return 0;
-    }
-    pos = (int)prior;
-    return pos + 1;
-  } else {
-    int64_t L = p.lens[b];
-    if (L < 0 || L > cap) {
-      set_err(p.err, CIE_ERRBIT_LEN);
-      L = L < 0 ? 0 : cap;
-    }
-    return (int)L;
-  }
-}
 
 // Append mode: point the lanes that hold key `pos` at the new rows instead of
 // the pool, and after the loads land, store those rows into the pool.
@@ -173,6 +151,36 @@ __device__ __forceinline__ void store_new_row(const KVPair<D>& kv, const PagedSr
   }
 }
 
+// RoPE of the Q / K operand dims a lane holds (dims 8*grp + 32*ks + j, j < 8):
+// the partners i and i + D/2 of rotate_half sit in k-steps ks and ks + KS/2
+// of the same lane, so no lane exchange is needed.
+template <int D>
+__device__ __forceinline__ void rope_lane(f16x8 (&x)[Geo<D>::KS], const f16x8 (&c)[Geo<D>::KS],
+                                          const f16x8 (&s)[Geo<D>::KS]) {
+  constexpr int H = Geo<D>::KS / 2;
+#pragma unroll
+  for (int ks = 0; ks < H; ++ks) rope8(x[ks], x[ks + H], c[ks], c[ks + H], s[ks], s[ks + H]);
+}
+
+// Rope mode: put the rotated K row of the new token (knew, held by every lane
+// for its dims) into the lanes of its key in a loaded pair, replacing the
+// unrotated row the tile load read from k_new.  pos must lie in the pair.
+template <int D>
+__device__ __forceinline__ void put_new_k(KVPair<D>& kv, int key0a, int key0b, int pos,
+                                          const f16x8 (&knew)[Geo<D>::KS], int r16) {
+  const bool second = pos >= key0b;
+  const int row = pos - (second ? key0b : key0a);
+  // selects, not branches: a conditional write into the register-staged pair
+  // would make the compiler move the pair to scratch memory
+  const bool in_a = r16 == row && !second;
+  const bool in_b = r16 == row && second;
+#pragma unroll
+  for (int ks = 0; ks < Geo<D>::KS; ++ks) {
+    kv.k[0][ks] = in_a ? knew[ks] : kv.k[0][ks];
+    kv.k[1][ks] = in_b ? knew[ks] : kv.k[1][ks];
+  }
+}
+
 // Split partials cross workgroups (and XCDs, each with its own L2).  With the
 // fence-free merge they are written and read as agent-scope atomics
 // (global_store / global_load ... sc1), coherent device-wide.
@@ -222,8 +230,9 @@ constexpr int kTraceSlots = 24;
   } while (0)
 #endif
 
-template <int D, int WAVES, bool kAppend>
+template <int D, int WAVES, bool kAppend, bool kRope>
 __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
+  static_assert(kAppend || !kRope, "rope mode appends");
   constexpr int KS = Geo<D>::KS;
   constexpr int NT = Geo<D>::NT;
   __shared__ float sm_m[WAVES][16];
@@ -301,7 +310,7 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
 
   // Q^T operand: column r16 = head g*G + r16 (zero past the group).
   f16x8 qop[1][KS];
-  const f16* qrow = p.q + ((int64_t)b * p.H_q + g * p.G + r16) * D + 8 * grp;
+  const f16* qrow = p.q + (int64_t)b * p.q_row_stride + (int64_t)(g * p.G + r16) * D + 8 * grp;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
     qop[0][ks] = (r16 < p.G) ? *reinterpret_cast<const f16x8*>(qrow + 32 * ks) : f16x8{};
@@ -313,6 +322,22 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
     nr.k = p.k_new + (int64_t)b * p.k_tok_stride + (int64_t)g * p.k_head_stride;
     nr.v = p.v_new + (int64_t)b * p.v_tok_stride + (int64_t)g * p.v_head_stride;
     nr.pos = pos;
+  }
+  // Rope mode: rotate q now, and the new token's K row (every lane its dims)
+  // for the lanes of that key to take once its tile is loaded.
+  f16x8 knew[KS];
+  if constexpr (kRope) {
+    f16x8 cs[KS], sn[KS];
+    const f16* crow = p.cos + (int64_t)b * p.cs_stride + 8 * grp;
+    const f16* srow = p.sin + (int64_t)b * p.cs_stride + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      cs[ks] = *reinterpret_cast<const f16x8*>(crow + 32 * ks);
+      sn[ks] = *reinterpret_cast<const f16x8*>(srow + 32 * ks);
+      knew[ks] = *reinterpret_cast<const f16x8*>(nr.k + 8 * grp + 32 * ks);
+    }
+    rope_lane<D>(qop[0], cs, sn);
+    rope_lane<D>(knew, cs, sn);
   }
 
   DECODE_TRACE(1, __builtin_amdgcn_s_memrealtime());
@@ -351,6 +376,9 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   }
   auto attend_odd = [&]() {
     if (xkey + 16 >= L) zero_tail_rows<D>(xt, xkey, kNoKey, L, grp);
+    if constexpr (kRope) {
+      if (pos >= xkey && pos < xkey + 16) put_new_k<D>(xt, xkey, kNoKey, pos, knew, r16);
+    }
     attend_pair<D, 1>(st, xt, QRegs<D, 1>{qop}, xkey, kNoKey, lim, L, p.scale_log2, grp);
   };
 
@@ -404,7 +432,10 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
             zero_tail_rows<D>(cur, ka, kb, L, grp);
             if constexpr (kAppend) {
               // the new token is the sequence's last key: it sits in this pair
-              if (pos >= ka) store_new_row<D>(cur, src, loc[u][0], loc[u][1], ka, kb, pos, r16, grp);
+              if (pos >= ka) {
+                if constexpr (kRope) put_new_k<D>(cur, ka, kb, pos, knew, r16);
+                store_new_row<D>(cur, src, loc[u][0], loc[u][1], ka, kb, pos, r16, grp);
+              }
             }
           }
           attend_pair<D, 1>(st, cur, QRegs<D, 1>{qop}, ka, kb, lim, L, p.scale_log2, grp);
@@ -581,11 +612,11 @@ constexpr int decode_waves() {
   return D <= 64 ? CIE_DECODE_WAVES : (CIE_DECODE_WAVES > 4 ? 4 : CIE_DECODE_WAVES);
 }
 
-template <int D, bool kAppend>
+template <int D, bool kAppend, bool kRope>
 static int launch_decode(const DecodeParams& p, hipStream_t stream) {
   constexpr int W = decode_waves<D>();
   dim3 grid(p.n_splits, p.H_kv, p.B);
-  hipLaunchKernelGGL((decode_kernel<D, W, kAppend>), grid, dim3(W * kWave), 0, stream, p);
+  hipLaunchKernelGGL((decode_kernel<D, W, kAppend, kRope>), grid, dim3(W * kWave), 0, stream, p);
   int rc = (int)hipGetLastError();
 #if CIE_DECODE_MERGE == 3
   if (rc == 0 && p.n_splits > 1) {
@@ -612,7 +643,7 @@ static PartLayout part_layout(int64_t B, int64_t H_q, int64_t D, int64_t S) {
   return w;
 }
 
-template <bool kAppend>
+template <bool kAppend, bool kRope>
 static int decode_entry(DecodeParams& p, void* partials, int32_t* counters, int64_t B,
                         int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size, int64_t n_pages,
                         int64_t pool_page_stride, int64_t pool_head_stride, int64_t bt_stride,
@@ -658,7 +689,7 @@ static int decode_entry(DecodeParams& p, void* partials, int32_t* counters, int6
   p.scale_log2 = kLog2e / __builtin_sqrtf((float)D);
   p.err = err;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return D == 64 ? launch_decode<64, kAppend>(p, s) : launch_decode<128, kAppend>(p, s);
+  return D == 64 ? launch_decode<64, kAppend, kRope>(p, s) : launch_decode<128, kAppend, kRope>(p, s);
 }
 
 }  // namespace cie
@@ -685,10 +716,11 @@ extern "C" int cie_paged_decode(void* o, const void* q, const void* k_pool, cons
   p.q = static_cast<const f16*>(q);
   p.k_pool = const_cast<f16*>(static_cast<const f16*>(k_pool));
   p.v_pool = const_cast<f16*>(static_cast<const f16*>(v_pool));
+  p.q_row_stride = H_q * D;
   p.lens = lens;
   p.slot_ids = slot_ids;
   p.block_table = block_table;
-  return decode_entry<false>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages, pool_page_stride,
+  return decode_entry<false, false>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages, pool_page_stride,
                              pool_head_stride, bt_stride, bt_width, n_slots, n_splits, err,
                              stream);
 }
@@ -716,10 +748,49 @@ extern "C" int cie_paged_decode_append(
   p.k_head_stride = k_head_stride;
   p.v_tok_stride = v_tok_stride;
   p.v_head_stride = v_head_stride;
+  p.q_row_stride = H_q * D;
   p.lens = lens;
   p.slot_ids = slot_ids;
   p.block_table = block_table;
-  return decode_entry<true>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages, pool_page_stride,
-                            pool_head_stride, bt_stride, bt_width, n_slots, n_splits, err,
-                            stream);
+  return decode_entry<true, false>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages,
+                                   pool_page_stride, pool_head_stride, bt_stride, bt_width,
+                                   n_slots, n_splits, err, stream);
+}
+
+extern "C" int cie_paged_decode_qkv_rope(
+    void* o, const void* qkv, int64_t qkv_row_stride, const void* cos, const void* sin,
+    int64_t cs_row_stride, void* k_pool, void* v_pool, const int64_t* lens,
+    const int64_t* slot_ids, const int64_t* block_table, void* partials, int32_t* counters,
+    int64_t B, int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size, int64_t n_pages,
+    int64_t pool_page_stride, int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
+    int64_t n_slots, int64_t n_splits, int32_t* err, void* stream) {
+  if (B < 0 || H_q <= 0 || H_kv <= 0 || D <= 0) return CIE_EINVAL;
+  if (B > 0 && (!qkv || !cos || !sin)) return CIE_EINVAL;
+  if (((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(cos) |
+        reinterpret_cast<uintptr_t>(sin)) & 15) ||
+      qkv_row_stride % 8 != 0 || cs_row_stride % 8 != 0 ||
+      qkv_row_stride < (H_q + 2 * H_kv) * D || cs_row_stride < D)
+    return CIE_EINVAL;
+  const f16* base = static_cast<const f16*>(qkv);
+  DecodeParams p{};
+  p.o = static_cast<f16*>(o);
+  p.q = base;
+  p.q_row_stride = qkv_row_stride;
+  p.cos = static_cast<const f16*>(cos);
+  p.sin = static_cast<const f16*>(sin);
+  p.cs_stride = cs_row_stride;
+  p.k_pool = static_cast<f16*>(k_pool);
+  p.v_pool = static_cast<f16*>(v_pool);
+  p.k_new = base + H_q * D;
+  p.v_new = base + (H_q + H_kv) * D;
+  p.k_tok_stride = qkv_row_stride;
+  p.k_head_stride = D;
+  p.v_tok_stride = qkv_row_stride;
+  p.v_head_stride = D;
+  p.lens = lens;
+  p.slot_ids = slot_ids;
+  p.block_table = block_table;
+  return decode_entry<true, true>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages,
+                                  pool_page_stride, pool_head_stride, bt_stride, bt_width,
+                                  n_slots, n_splits, err, stream);
 }

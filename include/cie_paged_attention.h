@@ -143,6 +143,53 @@ int cie_paged_decode_append(void* o, const void* q, void* k_pool, void* v_pool,
                             void* stream);
 
 /*
+ * Decode step from the fused QKV projection, RoPE and KV append fused in, one
+ * launch.  Row b of qkv (qkv_row_stride elements apart, 16-byte aligned)
+ * holds q (H_q heads), then k (H_kv), then v (H_kv), D each; cos / sin rows b
+ * (cs_row_stride apart) are the new token's rotary tables.  q and k are
+ * rotated in registers as transformers' apply_rotary_pos_emb does
+ * (x*cos + rotate_half(x)*sin, computed in fp32, rounded once to fp16), the
+ * rotated k and v rows are appended at pos = lens[slot_ids[b]], and o is the
+ * decode attention of the rotated q over the pos + 1 tokens.
+ * Replaces the decode branch of TritonQwen2Attention.forward
+ * (attn/core.py:181-215): the QKV split, apply_rotary_pos_emb,
+ * KVStorage.decode_update and gqa_decode_attention.  Other arguments as for
+ * cie_paged_decode_append.
+ */
+int cie_paged_decode_qkv_rope(void* o, const void* qkv, int64_t qkv_row_stride,
+                              const void* cos, const void* sin, int64_t cs_row_stride,
+                              void* k_pool, void* v_pool,
+                              const int64_t* lens, const int64_t* slot_ids,
+                              const int64_t* block_table, void* partials,
+                              int32_t* counters,
+                              int64_t B, int64_t H_q, int64_t H_kv, int64_t D,
+                              int64_t page_size, int64_t n_pages,
+                              int64_t pool_page_stride, int64_t pool_head_stride,
+                              int64_t bt_stride, int64_t bt_width, int64_t n_slots,
+                              int64_t n_splits, int32_t* err, void* stream);
+
+/*
+ * Token-mode append from the fused QKV projection, with RoPE: for each packed
+ * token t < T (row t of qkv, layout as for cie_paged_decode_qkv_rope; cos /
+ * sin row t), the rotated q heads go to q_out (T, H_q, D) dense, and the
+ * rotated k and the v rows to (pages[t], head, offsets[t]) of the pools.
+ * Replaces the mixed branch's QKV split, apply_rotary_pos_emb and
+ * KVStorage.mixed_update (attn/core.py:181-198, 226-229;
+ * kv_cache/storage.py:62-85).  D must be a multiple of 16; every pointer
+ * 16-byte aligned.
+ */
+int cie_kv_append_tokens_qkv_rope(void* q_out, void* k_pool, void* v_pool,
+                                  const void* qkv, int64_t qkv_row_stride,
+                                  const void* cos, const void* sin,
+                                  int64_t cs_row_stride,
+                                  const int64_t* pages, const int64_t* offsets,
+                                  int64_t T, int64_t H_q, int64_t H_kv,
+                                  int64_t page_size, int64_t D, int64_t n_pages,
+                                  int64_t pool_page_stride,
+                                  int64_t pool_head_stride, int32_t* err,
+                                  void* stream);
+
+/*
  * Varlen causal GQA attention over the paged pool for a packed batch of
  * chunked-prefill and decode sequences.  Sequence b owns query rows
  * [cu_seqlens[b], cu_seqlens[b+1]); its row i sits at absolute position

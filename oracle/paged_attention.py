@@ -16,13 +16,17 @@ CPU (attention arithmetic):
   decode_attention_splitkv kernels/decode_attention.py:71-141 (interleaved splits,
                            fp16 P) + :243-264 (log-sum-exp merge, -inf guard)
   mixed_attention          attn/core.py:69-111 + kernels/prefill_attention.py:37-198
+  rope                     attn/core.py:193-198 (transformers' apply_rotary_pos_emb),
+                           in fp32, rounded once to fp16
   *_bruteforce             scalar Python loops of the same definitions (tiny inputs)
 
 Pins (tests/test_oracle.py): brute-force loops, torch's
 ``scaled_dot_product_attention`` (a library routine) on contiguous K/V, closed
 forms (single key -> v0, equal keys -> mean of V, empty -> 0), invariants (page
 permutation, split count, L=1 mixed == decode), and planted mistakes that the
-pins must catch.
+pins must catch.  ``rope`` is pinned against transformers'
+``apply_rotary_pos_emb`` run in fp32 (a library routine), the identity at
+angle 0 and the 2-D rotation closed form.
 """
 from __future__ import annotations
 
@@ -31,6 +35,23 @@ import math
 import numpy as np
 import torch
 import torch.nn.functional as F
+
+
+# ----------------------------------------------------------------------------- rope
+
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x*cos + rotate_half(x)*sin of apply_rotary_pos_emb (attn/core.py:193-198).
+
+    x (T, H, D) fp16; cos / sin (T, D) fp16 (the rotary tables of each token's
+    position); rotate_half(x) = cat(-x[..., D/2:], x[..., :D/2]).  The products
+    of fp16 values are exact in fp32, so computing in fp32 rounds each output
+    once (then to fp16) — what a fused fp32 kernel (or torch.compile's) stores.
+    """
+    xf = x.float()
+    c, s = cos.float()[:, None, :], sin.float()[:, None, :]
+    half = xf.shape[-1] // 2
+    rot = torch.cat([-xf[..., half:], xf[..., :half]], dim=-1)
+    return (xf * c + rot * s).half()
 
 
 # ----------------------------------------------------------------------------- append

@@ -23,6 +23,7 @@ def test_header_declares_the_hot_path():
     for want in ("cie_kv_append_decode", "cie_kv_append_tokens", "cie_paged_decode",
                  "cie_paged_decode_append", "cie_paged_decode_max_splits",
                  "cie_paged_decode_partials_bytes", "cie_mixed_attention",
+                 "cie_paged_decode_qkv_rope", "cie_kv_append_tokens_qkv_rope",
                  "cie_mixed_partials_bytes", "cie_mixed_counters", "cie_abi_version",
                  "cie_status_string"):
         assert want in names
@@ -125,3 +126,28 @@ def test_append_and_mixed_reject_bad_arguments(native_lib):
     # mixed: counters are required
     assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, None, 1, 4, 4, 14, 2, 64, 16, 10,
                                    1024, 1024, 10, 10, 2, None, None) == -1
+
+
+def _call_decode_rope(lib, qkv_stride=1152, cos=32, cs_stride=64, B=1, D=64):
+    # fake, never-dereferenced device addresses: must fail validation on the host
+    return lib.cie_paged_decode_qkv_rope(144, 16, qkv_stride, cos, 48, cs_stride, 64, 80, 96, 112, 128,
+                                         160, 176, B, 14, 2, D, 16, 64, 2048, 1024, 64, 64, 2, 4,
+                                         None, None)
+
+
+def _call_tokens_rope(lib, qkv=16, T=3, D=64, qkv_stride=1152):
+    return lib.cie_kv_append_tokens_qkv_rope(144, 64, 80, qkv, qkv_stride, 32, 48, 64, 96, 112, T, 14, 2,
+                                             16, D, 64, 2048, 1024, None, None)
+
+
+def test_rope_entry_points_reject_bad_arguments_without_launching(native_lib):
+    lib = native_lib
+    assert _call_decode_rope(lib, qkv_stride=64) == -1      # row stride below q|k|v width
+    assert _call_decode_rope(lib, qkv_stride=1156) == -1    # row stride not a multiple of 8
+    assert _call_decode_rope(lib, cos=40) == -1             # cos not 16-byte aligned
+    assert _call_decode_rope(lib, cs_stride=32) == -1       # cos row shorter than D
+    assert _call_decode_rope(lib, B=0) == 0                 # empty batch: no-op
+    assert _call_tokens_rope(lib, D=72, qkv_stride=1296) == -2  # D not a multiple of 16
+    assert _call_tokens_rope(lib, qkv=24) == -1             # qkv not 16-byte aligned
+    assert _call_tokens_rope(lib, T=0) == 0                 # no tokens: no-op
+    assert _call_tokens_rope(lib, T=-1) == -1

@@ -34,7 +34,8 @@ def _hf_attention(attn32, rope32, hidden32, positions):
     return out
 
 
-def test_qwen2_attention_dropin_prefill_then_decode(native_lib):
+@pytest.mark.parametrize("fuse_rope,fuse_append", [(True, True), (False, True), (False, False)])
+def test_qwen2_attention_dropin_prefill_then_decode(native_lib, fuse_rope, fuse_append):
     torch.manual_seed(0)
     cfg = _config()
     attn_ref = Qwen2Attention(cfg, layer_idx=1).float()
@@ -43,6 +44,7 @@ def test_qwen2_attention_dropin_prefill_then_decode(native_lib):
             p.normal_(0, 0.05)
     rope32 = Qwen2RotaryEmbedding(cfg)
     ours = TritonQwen2Attention(copy.deepcopy(attn_ref).half().to(DEV)).to(DEV)
+    ours.fuse_rope, ours.fuse_append = fuse_rope, fuse_append
     rope16 = Qwen2RotaryEmbedding(cfg, device=DEV)
 
     kv = KVStorage(cfg, max_cache_len=1024, page_size=16, n_slots=4, device=DEV, dtype=torch.float16)

@@ -301,3 +301,48 @@ def test_algorithmic_bytes_headline():
     assert ref.decode_algorithmic_bytes([4097] * 32, 14, 2, 64, 16) == 67_339_008
     assert ref.decode_algorithmic_bytes([16385] * 16, 14, 2, 64, 16) == 134_431_104
     assert ref.decode_algorithmic_bytes([129], 14, 2, 64, 16) == 70_744
+
+
+# ----------------------------------------------------------------------------- rope
+
+def _rope_inputs(seed, T=5, H=3, D=64):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(T, H, D, generator=g) * 2).half()
+    ang = torch.rand(T, D // 2, generator=g, dtype=torch.float64) * 50
+    ang = torch.cat([ang, ang], dim=-1)
+    return x, ang.cos().half(), ang.sin().half()
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_rope_matches_transformers_apply_rotary_pos_emb(seed):
+    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+    x, cos, sin = _rope_inputs(seed)
+    # transformers layout: (batch, heads, T, D) with cos / sin (batch, T, D)
+    q = x.float().permute(1, 0, 2)[None]
+    qe, _ = apply_rotary_pos_emb(q, q, cos.float()[None], sin.float()[None], unsqueeze_dim=1)
+    want = qe[0].permute(1, 0, 2).half()
+    assert torch.equal(ref.rope(x, cos, sin), want)
+
+
+def test_rope_identity_at_angle_zero_and_rotation_closed_form():
+    x, _, _ = _rope_inputs(2)
+    T, H, D = x.shape
+    one, zero = torch.ones(T, D).half(), torch.zeros(T, D).half()
+    assert torch.equal(ref.rope(x, one, zero), x)
+    # a quarter turn maps (a, b) -> (-b, a) exactly
+    y = ref.rope(x, zero, one)
+    half = D // 2
+    assert torch.equal(y[..., :half], -x[..., half:])
+    assert torch.equal(y[..., half:], x[..., :half])
+
+
+def test_rope_pin_catches_a_flipped_rotate_half():
+    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+    x, cos, sin = _rope_inputs(3)
+    xf = x.float()
+    half = xf.shape[-1] // 2
+    wrong = (xf * cos.float()[:, None] + torch.cat([xf[..., half:], -xf[..., :half]], -1)
+             * sin.float()[:, None]).half()
+    q = x.float().permute(1, 0, 2)[None]
+    qe, _ = apply_rotary_pos_emb(q, q, cos.float()[None], sin.float()[None], unsqueeze_dim=1)
+    assert not torch.equal(wrong, qe[0].permute(1, 0, 2).half())
