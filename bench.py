@@ -414,19 +414,23 @@ def bench_mixed(args, cie, inputs, ref, dev):
     }), flush=True)
 
 
-def bench_model(args, cie, dev, batch: int = 32, new_tokens: int = 128, budget: int = 512,
-                sigma: float = 0.5):
-    """Config 5: a 24-layer Qwen2.5-0.5B-shaped model (random fp16 weights) through the drop-in.
+def bench_model(args, cie, dev, n_requests: int = 64, n_slots: int = 33, new_tokens: int = 128,
+                budget: int = 512, sigma: float = 0.5):
+    """Config 5: a 24-layer Qwen2.5-0.5B-shaped model (random fp16 weights) served end to end.
 
-    B requests (prompt lengths lognormal, median 256, sigma recorded, clipped
-    to [16, 2048]) are prefilled by MixedModule in steps of at most `budget`
-    tokens (chunked prefill), then decoded for `new_tokens` steps by
-    DecodeModule (one hipGraph replay per step: every layer's fused append +
-    paged decode).  Reported: decode tokens/s and step time, graph replay
-    alone, the attention launches of one step alone, prefill tokens/s.
+    Continuous batching (``Scheduler``, the reference's policy): `n_requests`
+    prompts (lognormal lengths, median 256, sigma recorded, clipped to
+    [16, 2048]) through `n_slots - 1` slots, a token budget of `budget` per
+    step and a 32,768-token pool; each request generates `new_tokens` tokens
+    (no EOS: random weights).  Prefill chunks and decode rows are packed into
+    eager mixed steps; pure decode steps replay the hipGraph of the batch
+    bucket (every layer: one rope + append + split-KV decode launch).
+    Reported: output tokens/s over the whole run (the metric), steps,
+    preemptions; then, on 32 resident sequences, the steady-state decode step,
+    its graph replay alone and the attention launches of one step alone.
     """
     from transformers import Qwen2Config, Qwen2ForCausalLM
-    from custom_inference_engine_amd.scheduler import DecodeModule, MixedModule, assign_pages
+    from custom_inference_engine_amd.scheduler import Scheduler, assign_pages
 
     cfg = Qwen2Config(hidden_size=896, num_attention_heads=14, num_key_value_heads=2, intermediate_size=4864,
                       num_hidden_layers=24, vocab_size=151936, max_position_embeddings=32768, rope_theta=1e6,
@@ -437,87 +441,116 @@ def bench_model(args, cie, dev, batch: int = 32, new_tokens: int = 128, budget: 
         model = Qwen2ForCausalLM(cfg)
     model = model.half().eval()
     cie.use_triton_attention(model)
-    kv = cie.KVStorage(cfg, max_cache_len=32768, page_size=16, n_slots=batch + 1, device=dev,
+    kv = cie.KVStorage(cfg, max_cache_len=32768, page_size=16, n_slots=n_slots, device=dev,
                        dtype=torch.float16)
-    log(f"config 5: 24 layers, B={batch}, pool {kv.n_pages} pages; capturing the decode step graph")
-    dec = DecodeModule(model, kv, batch_size=batch)
-    mix = MixedModule(model, kv, token_count=budget)
+    log(f"config 5: 24 layers, {n_requests} requests, {n_slots - 1} slots, pool {kv.n_pages} pages; "
+        f"capturing the decode graphs")
+    t0 = time.perf_counter()
+    sched = Scheduler(model, kv, eos_token_ids={cfg.vocab_size}, max_new_tokens=new_tokens,
+                      token_budget=budget)
+    init_s = time.perf_counter() - t0
+
+    # time every step as the loop sees it (each ends in a host sync: .tolist())
+    ex = sched.executor
+    step_time = {"decode": [], "mixed": []}
+
+    def timed(kind, fn):
+        def run(*a):
+            t = time.perf_counter()
+            out = fn(*a)
+            step_time[kind].append((len(a[-1]), time.perf_counter() - t))
+            return out
+        return run
+    ex.decode, ex.mixed = timed("decode", ex.decode), timed("mixed", ex.mixed)
 
     g = torch.Generator().manual_seed(5)
-    lens = torch.exp(torch.randn(batch, generator=g) * sigma + math.log(256)).round().clamp(16, 2048).long()
+    lens = torch.exp(torch.randn(n_requests, generator=g) * sigma + math.log(256)).round().clamp(16, 2048).long()
     prompts = [torch.randint(0, cfg.vocab_size, (int(n),), generator=g).tolist() for n in lens]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.inference_mode():
+        results = sched.generate(prompts)
+    torch.cuda.synchronize()
+    run_s = time.perf_counter() - t0
+    n_out = sum(len(r.new_tokens) for r in results)
+    n_prompt = int(lens.sum())
+    st = sched.stats
+    dec32 = [dt for n, dt in step_time["decode"] if n == n_slots - 1]
+    ttft = sorted(r.t_first - r.t_arrival for r in results)
+    log(f"served {n_requests} requests: {n_prompt} prompt + {n_out} output tokens in {run_s:.2f} s; "
+        f"{sum(st.decode_steps.values())} decode + {sum(st.mixed_steps.values())} mixed steps, "
+        f"{st.preemptions} preemptions")
+
+    # steady state on 32 resident sequences (the bucket-32 graph of the same executor)
+    batch = n_slots - 1
+    dec = ex.decode_module(batch)
     slots = list(range(1, batch + 1))
     free = (torch.randperm(kv.n_pages - 1, generator=g) + 1).tolist()
-    extra = 64  # decode tokens beyond new_tokens (the replay-only timing)
-    for sl, p in zip(slots, prompts):
+    extra = 64
+    for sl, p in zip(slots, prompts[:batch]):
         assign_pages(kv, sl, len(p) + new_tokens + extra, free)
-
-    # chunked prefill: each step packs up to `budget` tokens of the pending prompts
-    done = [0] * batch
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    n_steps = 0
-    while any(d < len(p) for d, p in zip(done, prompts)):
-        chunk, chunk_slots, left = [], [], budget
-        for i, p in enumerate(prompts):
-            if done[i] < len(p) and left > 0:
-                n = min(len(p) - done[i], left)
-                chunk.append(p[done[i]:done[i] + n])
-                chunk_slots.append(slots[i])
-                done[i] += n
-                left -= n
-        mix.forward(chunk, chunk_slots)
-        n_steps += 1
-    torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
-    n_prompt = int(lens.sum())
-    log(f"prefill: {n_prompt} tokens in {n_steps} steps, {prefill_s * 1e3:.1f} ms")
-
-    # decode: full step (upload + replay + argmax + host sync), as the reference's DecodeModule.forward
-    for _ in range(3):
-        dec.forward(slots)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(new_tokens - 3):
-        dec.forward(slots)
-    torch.cuda.synchronize()
-    step_us = (time.perf_counter() - t0) / (new_tokens - 3) * 1e6
-    # graph replay alone
-    n_rep = extra - 8
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.inference_mode():
+        done = [0] * batch
+        while any(d < len(p) for d, p in zip(done, prompts)):
+            chunk, chunk_slots, left = [], [], budget
+            for i, p in enumerate(prompts[:batch]):
+                if done[i] < len(p) and left > 0:
+                    n = min(len(p) - done[i], left)
+                    chunk.append(p[done[i]:done[i] + n])
+                    chunk_slots.append(slots[i])
+                    done[i] += n
+                    left -= n
+            if not chunk:
+                break
+            ex.mixed_module(sum(map(len, chunk))).forward(chunk, chunk_slots)
+        for _ in range(3):
+            dec.forward(slots)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(new_tokens - 3):
+            dec.forward(slots)
+        torch.cuda.synchronize()
+        step_us = (time.perf_counter() - t0) / (new_tokens - 3) * 1e6
+        n_rep = extra - 8
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(n_rep):
             dec.graph.replay()
         end.record()
-    torch.cuda.synchronize()
-    replay_us = start.elapsed_time(end) * 1e3 / n_rep
-    # the attention launches of one step alone: 24 fused append + decode calls on the live pools
-    with torch.inference_mode():
-        q = torch.randn(1, batch, 14, 64, device=dev, dtype=torch.float16)
-        kn = torch.randn(1, batch, 2, 64, device=dev, dtype=torch.float16)
-    slot_t = torch.tensor(slots, device=dev)
+        torch.cuda.synchronize()
+        replay_us = start.elapsed_time(end) * 1e3 / n_rep
+        # the attention launches of one step alone: 24 one-launch rope + append + decode calls
+        qkv = torch.randn(1, batch, (14 + 4) * 64, device=dev, dtype=torch.float16)
+        cos = torch.ones(1, batch, 64, device=dev, dtype=torch.float16)
+        sin = torch.zeros(1, batch, 64, device=dev, dtype=torch.float16)
+        slot_t = torch.tensor(slots, device=dev)
 
-    def attn_step():
-        for layer in range(cfg.num_hidden_layers):
-            cie.decode_append_gqa_attention(q, kv.keys[layer], kv.values[layer], kn, kn, kv.lens, slot_t,
-                                            kv.block_table)
-    with torch.inference_mode():  # the step modules made the RNG's graph state an inference tensor
+        def attn_step():
+            for layer in range(cfg.num_hidden_layers):
+                cie.decode_qkv_rope_gqa_attention(qkv, cos, sin, kv.keys[layer], kv.values[layer], kv.lens,
+                                                  slot_t, kv.block_table, num_heads=14)
         attn_us, _ = time_calls([attn_step], 40, 8, True, 3)
     ctx = float((kv.lens[slots].float().mean()).item())
     line = {
-        "metric": "config 5 decode tokens/s (24-layer Qwen2.5-0.5B shape, B=32, hipGraph decode step)",
-        "value": round(batch / (step_us * 1e-6), 1), "unit": "tokens/s", "higher_is_better": True,
-        "n_gpus": 1, "steps": new_tokens, "ms_per_step": round(step_us / 1e3, 4),
-        "decode_step_us": round(step_us, 1), "graph_replay_us": round(replay_us, 1),
-        "attention_us_per_step": round(attn_us, 1),
-        "attention_share_of_replay": round(attn_us / replay_us, 3),
-        "prefill_tokens_per_s": round(n_prompt / prefill_s, 1),
+        "metric": "config 5 output tokens/s (24-layer Qwen2.5-0.5B shape, continuous batching of 64 requests)",
+        "value": round(n_out / run_s, 1), "unit": "tokens/s", "higher_is_better": True,
+        "n_gpus": 1, "steps": sum(st.decode_steps.values()) + sum(st.mixed_steps.values()),
+        "wall_s": round(run_s, 3), "init_s": round(init_s, 2),
+        "total_tokens_per_s": round((n_out + n_prompt) / run_s, 1),
+        "decode_steps": sum(st.decode_steps.values()), "mixed_steps": sum(st.mixed_steps.values()),
+        "preemptions": st.preemptions, "recomputed_tokens": st.recomputed_tokens,
+        "decode_step_ms_at_b32_in_run": round(sorted(dec32)[len(dec32) // 2] * 1e3, 3) if dec32 else None,
+        "ttft_ms_median": round(ttft[len(ttft) // 2] * 1e3, 1),
+        "steady_state_b32": {"decode_step_us": round(step_us, 1), "tokens_per_s": round(batch / (step_us * 1e-6), 1),
+                             "graph_replay_us": round(replay_us, 1), "attention_us_per_step": round(attn_us, 1),
+                             "attention_share_of_replay": round(attn_us / replay_us, 3),
+                             "mean_context": round(ctx, 1)},
         "dtype": "fp16 (fp32 accumulate)", "data": "synthetic (random weights, random prompt ids)",
-        "config": {"workload": "Qwen2.5-0.5B-shaped forward, random init from a local Qwen2Config",
-                   "layers": 24, "batch": batch, "prompt_len_median": 256, "prompt_len_sigma": sigma,
-                   "prompt_tokens": n_prompt, "new_tokens": new_tokens, "token_budget": budget,
-                   "prefill_steps": n_steps, "pool_tokens": 32768, "mean_context_at_end": round(ctx, 1)},
+        "config": {"workload": "Qwen2.5-0.5B-shaped forward, random init from a local Qwen2Config, "
+                               "reference scheduling policy",
+                   "layers": 24, "requests": n_requests, "slots": n_slots - 1, "prompt_len_median": 256,
+                   "prompt_len_sigma": sigma, "prompt_tokens": n_prompt, "new_tokens": new_tokens,
+                   "token_budget": budget, "pool_tokens": 32768},
     }
     print(json.dumps(line), flush=True)
 
