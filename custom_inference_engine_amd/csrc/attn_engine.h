@@ -353,12 +353,19 @@ struct PagedSrc {
 // Tiles are read through per-tile buffer descriptors (tile_rsrc), so keys at
 // or past key_end read as zeros.
 // key_end = number of keys that exist (rows at or past it are zeroed).
-template <int D, int NCT, int PF, class QS>
+// prologue() runs once, after the first page-id loads are issued and before
+// any K/V load (or at once when the wave has no tiles): the caller stages
+// operands there (its Q), so their loads and the page ids' take one memory
+// round trip together.
+template <int D, int NCT, int PF, class QS, class Prologue>
 __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& qop,
                                              const int (&lim)[NCT], int t_begin, int t_end,
                                              int key_end, const PagedSrc& src, float scale_log2,
-                                             int r16, int grp) {
-  if (t_begin >= t_end) return;
+                                             int r16, int grp, Prologue prologue) {
+  if (t_begin >= t_end) {
+    prologue();
+    return;
+  }
   int mask_from = kNoKey;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) mask_from = min(mask_from, lim[c]);
@@ -367,10 +374,10 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
   const int lane = threadIdx.x & (kWave - 1);
   const int tpp = src.page_size >> 4;  // 16-key tiles per page
   const TileLaneOffsets<D> lanes(r16, grp);
-  for (int c0 = t_begin; c0 < t_end; c0 += kWave) {
-    const int n_chunk = min(kWave, t_end - c0);
+  // page ids of tiles c0 + lane, one per lane
+  auto lane_pages = [&](int c0) {
     int page = 0;
-    if (lane < n_chunk) {
+    if (lane < min(kWave, t_end - c0)) {
       int64_t pg = src.bt_row[(c0 + lane) / tpp];
       if (pg < 0 || pg >= src.n_pages) {
         set_err(src.err, CIE_ERRBIT_PAGE);
@@ -378,6 +385,13 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
       }
       page = (int)pg;
     }
+    return page;
+  };
+  int page = lane_pages(t_begin);
+  prologue();  // while the first page ids are in flight
+  for (int c0 = t_begin; c0 < t_end; c0 += kWave) {
+    const int n_chunk = min(kWave, t_end - c0);
+    if (c0 != t_begin) page = lane_pages(c0);
     const int n_pairs = (n_chunk + 1) >> 1;
     KVPair<D> ring[PF + 1];
     int keya[PF + 1], keyb[PF + 1];

@@ -237,22 +237,27 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
   int lim[NCT];
 #pragma unroll
   for (int c = 0; c < NCT; ++c) load_combo_q<D>(p, s, tp, g, ct0 + c, r16, grp, qop[c], lim[c]);
-  MIXED_TRACE(item, 9, __builtin_amdgcn_s_memrealtime());
   SoftmaxAcc<D, NCT> st;
   st.init();
   if constexpr (CIE_MIXED_QLDS) {
-    // this wave's block of Q operands in LDS (read back by this wave only)
+    // this wave's block of Q operands in LDS (read back by this wave only),
+    // written while the wave's first page ids are in flight: the Q loads and
+    // the page-id loads then share one memory round trip
     f16x8* mine = sm_q + wave * (col_group<D>() * KS * kWave);
     const int lane = threadIdx.x & (kWave - 1);
+    auto stage_q = [&]() {
 #pragma unroll
-    for (int c = 0; c < NCT; ++c)
+      for (int c = 0; c < NCT; ++c)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) mine[(c * KS + ks) * kWave + lane] = qop[c][ks];
+        for (int ks = 0; ks < KS; ++ks) mine[(c * KS + ks) * kWave + lane] = qop[c][ks];
+      MIXED_TRACE(item, 9, __builtin_amdgcn_s_memrealtime());
+    };
     stream_tiles<D, NCT, mixed_pf<D>()>(st, QLds<D>{mine, lane}, lim, w0, w1, tp.key_end, src,
-                                        p.scale_log2, r16, grp);
+                                        p.scale_log2, r16, grp, stage_q);
   } else {
+    MIXED_TRACE(item, 9, __builtin_amdgcn_s_memrealtime());
     stream_tiles<D, NCT, mixed_pf<D>()>(st, QRegs<D, NCT>{qop}, lim, w0, w1, tp.key_end, src,
-                                        p.scale_log2, r16, grp);
+                                        p.scale_log2, r16, grp, [] {});
   }
   MIXED_TRACE(item, 8, __builtin_amdgcn_s_memrealtime());
   const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
