@@ -94,12 +94,14 @@ def test_decode_qkv_rope_headline_shape(native_lib):
     assert torch.equal(bits(o2), bits(o1))
 
 
-@pytest.mark.parametrize("prior,new,pad", [
-    ([0, 37, 300], [20, 1, 45], 0),
-    ([5, 0, 1000, 64, 3], [1, 64, 17, 1, 33], 16),
+@pytest.mark.parametrize("prior,new,pad,h_q,h_kv,d", [
+    ([0, 37, 300], [20, 1, 45], 0, 14, 2, 64),
+    ([5, 0, 1000, 64, 3], [1, 64, 17, 1, 33], 16, 14, 2, 64),
+    ([3, 130], [40, 2], 0, 8, 2, 128),
+    ([0, 17], [19, 5], 8, 4, 4, 64),
 ])
-def test_append_tokens_qkv_rope_matches_oracle(native_lib, prior, new, pad):
-    case = inputs.make_case(prior, new, seed=9)
+def test_append_tokens_qkv_rope_matches_oracle(native_lib, prior, new, pad, h_q, h_kv, d):
+    case = inputs.make_case(prior, new, h_q=h_q, h_kv=h_kv, d=d, seed=9)
     T, H_q, D = case.q.shape[1:]
     seq = torch.repeat_interleave(torch.arange(len(prior)), case.new_lens)
     pos = case.kv_lens[seq] + (torch.arange(T) - case.cu_seqlens[seq])
