@@ -15,7 +15,7 @@ kernel: its per-launch time from HIP events on the stream it runs on, against
 (the reference's semantics: torch gather + SDPA in fp32, numpy append) on
 this host on a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--config 2|3|4] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--config 2|3|4|5|6] [--no-cpu-baseline]
     python bench.py --copy-calib      # plain copy kernel for rocprofv3 counter scaling
 """
 from __future__ import annotations
@@ -51,7 +51,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=800, help="decode calls timed (rounded up to a multiple of R)")
     ap.add_argument("--warmup", type=int, default=80)
-    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5))
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5, 6),
+                    help="6: the reference feature bench's mixed shape, beside its published times")
     ap.add_argument("--splits", type=int, default=None, help="KV splits (default: the library's policy)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of graph replay")
@@ -222,6 +223,8 @@ def main():
         return bench_mixed(args, cie, inputs, ref, dev)
     if args.config == 5:
         return bench_model(args, cie, dev)
+    if args.config == 6:
+        return bench_feature_shapes(args, cie, inputs, ref, dev)
     case = inputs.config2(seed=0) if args.config == 2 else inputs.config4(seed=0)
     splits = args.splits or (case.meta.get("n_splits") if args.config == 4 else None)
     log(f"config {args.config}: B={case.B} attend={int(case.attended[0])} pool pages={case.k_pool.shape[0]}")
@@ -411,6 +414,57 @@ def bench_mixed(args, cie, inputs, ref, dev):
                      "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
                      "traffic": TRAFFIC_BYTES[3][0], "traffic_source": TRAFFIC_BYTES[3][1]},
         "parity_max_abs_err": err,
+    }), flush=True)
+
+
+# mixed_gqa_attention_kernel us/call at T = 128 by batch size, RTX 4070 Laptop
+# (feature_bench/results/token_threshold/20261104-084454_full_graph_token_jump.json:1)
+PUBLISHED_MIXED_T128 = {1: 24.09, 2: 21.14, 4: 21.41, 8: 28.80, 16: 30.67, 32: 35.09}
+
+
+def bench_feature_shapes(args, cie, inputs, ref, dev, tokens: int = 128, context: int = 256):
+    """The reference feature bench's mixed step (feature_bench/full_graph_token_jump.py:19-22, 48-55).
+
+    B sequences share `tokens` new tokens (split evenly), each on `context`
+    cached tokens; one layer's mixed attention (the append is timed apart in
+    the reference too) with max_seqlen = the token count.  Pages here are
+    shuffled (the reference's bench assigns them contiguously).  Printed beside
+    the reference's published kernel times, measured on other hardware.
+    """
+    table = []
+    for B in sorted(PUBLISHED_MIXED_T128):
+        lens = [tokens // B + (1 if i < tokens % B else 0) for i in range(B)]
+        case = inputs.make_case([context] * B, lens, seed=B)
+        R = 8
+        layers = build_layers(case, dev, R)
+        c = case.to(dev)
+        for L in layers:
+            cie.kv_append_tokens(L.kp, L.vp, L.k_new, L.v_new, c.pages, c.offsets)
+        torch.cuda.synchronize()
+        o = cie.mixed_gqa_attention(layers[0].q, layers[0].kp, layers[0].vp, tokens, c.cu_seqlens, c.kv_lens,
+                                    c.slot_ids, c.block_table)
+        torch.cuda.synchronize()
+        want, written = ref.mixed_attention(case.q, layers[0].kp.cpu(), layers[0].vp.cpu(), case.cu_seqlens,
+                                            case.kv_lens, case.slot_ids, case.block_table)
+        err = (o[0].float().cpu() - want)[written].abs().max().item()
+
+        def call(i):
+            L = layers[i]
+            return lambda: cie.mixed_gqa_attention(L.q, L.kp, L.vp, tokens, c.cu_seqlens, c.kv_lens, c.slot_ids,
+                                                   c.block_table)
+        us, _ = time_calls([call(i) for i in range(R)], args.steps, args.warmup, not args.no_graph, args.repeats)
+        pub = PUBLISHED_MIXED_T128[B]
+        log(f"feature-bench shape B={B}: {us:.2f} us (reference, RTX 4070 Laptop: {pub} us), err {err:.1e}")
+        table.append({"batch": B, "us_per_call": round(us, 2), "published_us": pub,
+                      "speedup_vs_published": round(pub / us, 2), "parity_max_abs_err": err})
+    b32 = table[-1]
+    print(json.dumps({
+        "metric": "mixed attention us/call at the reference feature-bench shape (T=128, context 256)",
+        "value": b32["us_per_call"], "unit": "us/call", "higher_is_better": False, "n_gpus": 1,
+        "vs_published_rtx4070_laptop": b32["speedup_vs_published"], "table": table,
+        "dtype": "fp16 (fp32 accumulate)", "data": "synthetic (shuffled pages)",
+        "config": {"workload": "B sequences share 128 new tokens on 256 cached tokens each, one layer",
+                   "tokens": tokens, "context": context, "max_seqlen": tokens},
     }), flush=True)
 
 
