@@ -18,9 +18,9 @@ Policy per step (the reference's ``Scheduler.loop``, scheduler.py:508-653):
   admission stops.  Its page count rounds a page-aligned chunk up by one page
   (``_required_pages``, scheduler.py:209-218).
 * If any served request is prefilling, the step is one packed mixed step
-  (``MixedModule`` of the smallest token bucket that fits); otherwise a decode
-  step (``DecodeModule`` of the smallest batch bucket that fits, one hipGraph
-  replay) (scheduler.py:655-720).
+  (the mixed module of the smallest token bucket that fits: a graph replay
+  by default); otherwise a decode step (``DecodeModule`` of the smallest batch
+  bucket that fits, one hipGraph replay) (scheduler.py:655-720).
 * Afterwards each served request's KV length grows by its budget; a request
   whose prompt and generated tokens are all cached takes the step's token, and
   finishes on an EOS token or after ``max_new_tokens`` tokens, freeing its slot
@@ -120,16 +120,20 @@ def token_buckets(token_budget: int, min_bucket: int = 16, full_threshold: int =
 class ModuleExecutor:
     """Steps on the GPU through the step modules.
 
-    Every ``DecodeModule`` (one hipGraph per batch bucket) is captured here,
-    before any request runs: a module's warm-up writes through the slots it
-    covers and then resets them.  ``MixedModule`` instances (eager, static
-    buffers sized to a token bucket) are made on first use.
+    Every graph is captured here, before any request runs (a module's warm-up
+    writes through the slots it covers and then resets them): one
+    ``DecodeModule`` per batch bucket and, with ``graph_mixed``, one
+    ``FullMixedModule`` per token bucket at the largest batch bucket.
+    Without it, mixed steps run eagerly (``MixedModule`` of the token bucket,
+    made on first use).
     """
 
-    def __init__(self, model, kv_cache, batch_sizes: list[int], token_counts: list[int], pool=None):
+    def __init__(self, model, kv_cache, batch_sizes: list[int], token_counts: list[int], pool=None,
+                 graph_mixed: bool = True):
         import torch
 
         from .decode_module import DecodeModule
+        from .mixed_module import FullMixedModule
 
         self.model = model
         self.kv_cache = kv_cache
@@ -137,7 +141,12 @@ class ModuleExecutor:
         self.pool = pool if pool is not None else torch.cuda.graph_pool_handle()
         self.decode_modules = {b: DecodeModule(model, kv_cache, batch_size=b, pool=self.pool)
                                for b in sorted(batch_sizes, reverse=True)}
+        self.max_batch = max(batch_sizes)
         self.mixed_modules = {}
+        if graph_mixed:
+            for t in sorted(self.token_counts, reverse=True):
+                self.mixed_modules[t] = FullMixedModule(model, kv_cache, batch_size=self.max_batch,
+                                                        token_count=t, pool=self.pool)
 
     def decode_module(self, n: int):
         return self.decode_modules[_smallest_fit(self.decode_modules, n)]

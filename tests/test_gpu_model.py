@@ -75,3 +75,35 @@ def test_qwen2_model_mixed_prefill_then_graph_decode(native_lib):
             assert rel < 2e-2, f"decode step {step} seq {i}: rel err {rel:.3e}"
             seqs[i].append(nxt[i])
     assert kv.lens[slots].tolist() == [len(s) - 1 for s in seqs]
+
+
+def test_full_mixed_module_graph_matches_eager(native_lib):
+    """A prefill step replayed from FullMixedModule's graph (batch padded to 4 with the
+    reserved slot, cu_seqlens padded, max_seqlen = the bucket) equals the eager step."""
+    from custom_inference_engine_amd.scheduler import FullMixedModule
+
+    cfg, ref = _model()
+    ours = copy.deepcopy(ref).half().to(DEV)
+    use_triton_attention(ours)
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, 512, (n,), generator=g).tolist() for n in (37, 5, 20)]
+    slots = [1, 2, 3]
+    results = []
+    for graph in (False, True):
+        kv = KVStorage(cfg, max_cache_len=2048, page_size=16, n_slots=5, device=DEV, dtype=torch.float16)
+        note(f"mixed module, graph={graph}")
+        mod = (FullMixedModule(ours, kv, batch_size=4, token_count=64) if graph
+               else MixedModule(ours, kv, token_count=64))
+        free = (torch.randperm(kv.n_pages - 1, generator=torch.Generator().manual_seed(3)) + 1).tolist()
+        for s, p in zip(slots, prompts):
+            assign_pages(kv, s, len(p) + 8, free)
+        nxt = mod.forward(prompts, slots)
+        # a second, shorter step on top (decode rows through the mixed path)
+        nxt2 = mod.forward([[t] for t in nxt], slots)
+        torch.cuda.synchronize()
+        results.append((nxt, nxt2, mod.last_logits.float().cpu(), kv.lens.cpu(), kv.keys[0].cpu()))
+    (a1, a2, la, lens_a, k_a), (b1, b2, lb, lens_b, k_b) = results
+    assert a1 == b1 and a2 == b2
+    assert torch.equal(lens_a, lens_b) and lens_a[slots].tolist() == [len(p) + 1 for p in prompts]
+    assert torch.allclose(la, lb, rtol=1e-3, atol=1e-3)
+    assert torch.allclose(k_a[1:].float(), k_b[1:].float(), rtol=1e-3, atol=1e-3)  # page 0: padding
