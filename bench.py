@@ -309,6 +309,9 @@ def main():
 
     wl = ("paged GQA decode call = KV append + split-KV load + merge, one layer, one launch" if args.config == 2
           else "long-context paged GQA decode call (config 4)")
+    n_splits = splits or cie.attn.core.default_decode_splits(case.B, 2, dev)
+    # the library runs half-size (4-wave) workgroups when the grid exceeds one per CU
+    waves = 8 if n_splits * 2 * case.B <= torch.cuda.get_device_properties(dev).multi_processor_count else 4
     line = {
         "metric": METRIC if args.config == 2 else
         "long-context paged GQA decode us/call + HBM GB/s (% of peak) at B=16 kv_len=16384 (config 4)",
@@ -337,13 +340,13 @@ def main():
             "heads_q": 14, "heads_kv": 2, "head_dim": 64, "page_size": 16,
             "pool_pages_per_layer": int(case.k_pool.shape[0]),
             "layer_rotation": R,
-            "splits": splits or cie.attn.core.default_decode_splits(case.B, 2),
+            "splits": n_splits,
             "timing": "hipGraph replay of R calls" if use_graph else "eager launches",
             "algorithmic_bytes_per_call": bytes_call,
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel<64,8,true> (fused append + split-KV + merge, 1 launch/call)",
+            "kernel": f"decode_kernel<64,{waves},true> (fused append + split-KV + merge, 1 launch/call)",
             "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

@@ -606,18 +606,46 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
   merge_splits<D, 256>(p, blockIdx.y, blockIdx.x);
 }
 
-// Waves per workgroup: D = 128 needs twice the registers, so half the waves.
+// Waves per workgroup: a workgroup of decode_waves<D>() waves fills a CU's
+// wave slots at this kernel's register use (two waves per SIMD at D = 64; one
+// at D = 128, which needs twice the registers), so one workgroup per CU runs
+// at a time.  A grid with more workgroups than CUs would then run in rounds,
+// and the last round's stragglers set the call's time; such grids use
+// workgroups of half the waves instead, two per CU, all resident at once.
 template <int D>
 constexpr int decode_waves() {
   return D <= 64 ? CIE_DECODE_WAVES : (CIE_DECODE_WAVES > 4 ? 4 : CIE_DECODE_WAVES);
 }
 
+static int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static int cus[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+template <int D, int W, bool kAppend, bool kRope>
+static int launch_decode_waves(const DecodeParams& p, hipStream_t stream) {
+  dim3 grid(p.n_splits, p.H_kv, p.B);
+  hipLaunchKernelGGL((decode_kernel<D, W, kAppend, kRope>), grid, dim3(W * kWave), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
 template <int D, bool kAppend, bool kRope>
 static int launch_decode(const DecodeParams& p, hipStream_t stream) {
   constexpr int W = decode_waves<D>();
-  dim3 grid(p.n_splits, p.H_kv, p.B);
-  hipLaunchKernelGGL((decode_kernel<D, W, kAppend, kRope>), grid, dim3(W * kWave), 0, stream, p);
-  int rc = (int)hipGetLastError();
+  constexpr int Wh = W > 4 ? W / 2 : W;
+  const int64_t n_wg = (int64_t)p.n_splits * p.H_kv * p.B;
+  int rc = (Wh != W && n_wg > device_cus())
+               ? launch_decode_waves<D, Wh, kAppend, kRope>(p, stream)
+               : launch_decode_waves<D, W, kAppend, kRope>(p, stream);
 #if CIE_DECODE_MERGE == 3
   if (rc == 0 && p.n_splits > 1) {
     hipLaunchKernelGGL((decode_merge_kernel<D>), dim3(p.H_kv, p.B), dim3(256), 0, stream, p);
