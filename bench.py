@@ -288,6 +288,17 @@ def main():
     log(f"call, fused, eager launches: {us_eager:.2f} us")
     us_dec, _ = time_calls([decode_only(i) for i in range(R)], args.steps, args.warmup, use_graph, args.repeats)
     log(f"decode op alone (1 launch): {us_dec:.2f} us")
+    us_default = None
+    if splits is not None and args.splits is None:
+        # the config states its split count; the library's own choice beside it
+        def call_default(i):
+            L = layers[i]
+            return lambda: cie.decode_append_gqa_attention(L.q, L.kp, L.vp, L.k_new, L.v_new, lens_pool,
+                                                           slot_ids, bt)
+        us_default, _ = time_calls([call_default(i) for i in range(R)], args.steps, args.warmup, use_graph,
+                                   args.repeats)
+        log(f"call, fused, the library's default split count "
+            f"({cie.attn.core.default_decode_splits(case.B, 2, dev)}): {us_default:.2f} us")
 
     attended_list = case.attended.tolist()
     bytes_call = ref.decode_algorithmic_bytes(attended_list, 14, 2, 64, 16)
@@ -326,6 +337,7 @@ def main():
         "us_per_call_eager": round(us_eager, 3),
         "us_per_call_two_launch": round(us_two, 3),
         "us_decode_op_alone": round(us_dec, 3),
+        "us_per_call_default_splits": None if us_default is None else round(us_default, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
