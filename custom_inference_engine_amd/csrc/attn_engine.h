@@ -362,6 +362,11 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
                                              const int (&lim)[NCT], int t_begin, int t_end,
                                              int key_end, const PagedSrc& src, float scale_log2,
                                              int r16, int grp, Prologue prologue) {
+  // the bounds are wave-uniform: held in scalar registers, so the per-step
+  // tile bookkeeping below is scalar work
+  t_begin = uniform(t_begin);
+  t_end = uniform(t_end);
+  key_end = uniform(key_end);
   if (t_begin >= t_end) {
     prologue();
     return;
@@ -369,7 +374,9 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
   int mask_from = kNoKey;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) mask_from = min(mask_from, lim[c]);
-  // smallest limit over the wave's columns (wave-uniform)
+  // smallest limit over the wave's columns (wave-uniform; kept in a vector
+  // register: as a scalar it splits the masked and unmasked steps into
+  // separate paths and the step's registers spill)
   for (int off = 1; off < kWave; off <<= 1) mask_from = min(mask_from, __shfl_xor(mask_from, off, kWave));
   const int lane = threadIdx.x & (kWave - 1);
   const int tpp = src.page_size >> 4;  // 16-key tiles per page
@@ -387,11 +394,17 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
     }
     return page;
   };
+  // pool element offset of tile c0 + lane (page, head and in-page rows
+  // applied), computed once per 64 tiles so a step only reads two lanes
+  auto lane_offsets = [&](int c0, int page) {
+    return (int64_t)page * src.page_stride + src.head_off + (int64_t)(((c0 + lane) % tpp) * 16) * D;
+  };
   int page = lane_pages(t_begin);
   prologue();  // while the first page ids are in flight
   for (int c0 = t_begin; c0 < t_end; c0 += kWave) {
     const int n_chunk = min(kWave, t_end - c0);
     if (c0 != t_begin) page = lane_pages(c0);
+    const int64_t toff = lane_offsets(c0, page);
     const int n_pairs = (n_chunk + 1) >> 1;
     KVPair<D> ring[PF + 1];
     int keya[PF + 1], keyb[PF + 1];
@@ -403,15 +416,11 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
       j = min(j, n_pairs - 1);
       const int ka = 2 * j;  // chunk-local index of the step's first tile
       const bool two = ka + 1 < n_chunk;
-      const int ta = c0 + ka;
-      const int tb = two ? ta + 1 : ta;
-      const int pa = __builtin_amdgcn_readlane(page, ka);
-      const int pb = two ? __builtin_amdgcn_readlane(page, ka + 1) : pa;
-      const int key0a = ta * 16;
+      const int key0a = (c0 + ka) * 16;
       const int rows_a = real ? min(16, max(0, key_end - key0a)) : 0;
       const int rows_b = (real && two) ? min(16, max(0, key_end - key0a - 16)) : 0;
-      const int64_t oa = (int64_t)pa * src.page_stride + src.head_off + (int64_t)((ta % tpp) * 16) * D;
-      const int64_t ob = (int64_t)pb * src.page_stride + src.head_off + (int64_t)((tb % tpp) * 16) * D;
+      const int64_t oa = readlane64(toff, ka);
+      const int64_t ob = two ? readlane64(toff, ka + 1) : oa;
       typedef typename HVec<Geo<D>::NT>::type vrow_t;
       typedef vrow_t vquad_t[4];
       load_tile_buf<D>(ring[slot].k[0], *reinterpret_cast<vquad_t*>(&ring[slot].v[0]),

@@ -137,6 +137,12 @@ __device__ __forceinline__ bool arrive_last(int32_t* counter, int n_members, int
 __device__ __forceinline__ int uniform(int x) {
   return __builtin_amdgcn_readfirstlane(x);
 }
+// 64-bit value held by lane l (l wave-uniform).
+__device__ __forceinline__ int64_t readlane64(int64_t x, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)x, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)x >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ int64_t uniform64(int64_t x) {
   uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
   uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));

@@ -393,7 +393,7 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   constexpr int CG = col_group<D>();
   constexpr int W = mixed_waves<D>();
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = uniform(threadIdx.x / kWave);
   const int r16 = lane & 15;
   const int grp = lane >> 4;
   const TilePlan tp = tile_plan(qt, s, p.G, CG, W);
@@ -467,6 +467,10 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
   __shared__ int sm_last;
   __shared__ int sm_prefix[kMaxSeqs + 1];
   __shared__ int sm_scan[NTH];
+  // the plan's view of each sequence (seq_info), so an item starts its Q and
+  // page-id loads without reading the sequence tables again
+  __shared__ int64_t sm_t0[kMaxSeqs];
+  __shared__ int sm_slot[kMaxSeqs], sm_rows[kMaxSeqs], sm_prior[kMaxSeqs];
 
   constexpr int CG = col_group<D>();
   const int g = blockIdx.y;
@@ -477,21 +481,26 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     int n = 0;
     if (b < p.B) {
       const SeqInfo s = seq_info(p, b);
+      sm_t0[b] = s.t0;
+      sm_slot[b] = (int)s.slot;
+      sm_rows[b] = s.L;
+      sm_prior[b] = s.c;
       if (g == 0 && blockIdx.x == 0 && ((s.L + 15) >> 4) > p.n_qtiles)
         set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
       n = s.L > 0 ? seq_items(s, p.n_qtiles, p.G, CG, W) : 0;
     }
-    // inclusive block scan of n
+    // inclusive block scan of n over this pass's span of sequences
+    const int span = min(NTH, p.B - b0);
     sm_scan[threadIdx.x] = n;
     __syncthreads();
-    for (int off = 1; off < NTH; off <<= 1) {
+    for (int off = 1; off < span; off <<= 1) {
       const int add = threadIdx.x >= off ? sm_scan[threadIdx.x - off] : 0;
       __syncthreads();
       sm_scan[threadIdx.x] += add;
       __syncthreads();
     }
     if (b < p.B) sm_prefix[b + 1] = base + sm_scan[threadIdx.x];
-    base += sm_scan[NTH - 1];
+    base += sm_scan[span - 1];
     __syncthreads();
   }
   if (threadIdx.x == 0) sm_prefix[0] = 0;
@@ -511,7 +520,11 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
       else hi = mid;
     }
     const int b = uniform(lo);
-    const SeqInfo s = seq_info(p, b);
+    SeqInfo s;
+    s.t0 = uniform64(sm_t0[b]);
+    s.slot = uniform(sm_slot[b]);
+    s.L = uniform(sm_rows[b]);
+    s.c = uniform(sm_prior[b]);
     int j = item - uniform(sm_prefix[b]);
     int qt = 0;
     for (;; ++qt) {
