@@ -161,17 +161,26 @@ __device__ __forceinline__ void zero_tail_rows(KVPair<D>& kv, int key0a, int key
   }
 }
 
+// Reference max of a column that has seen no key: finite, so 2^(s - m) of a
+// masked score (s = -inf) is 0 with no special case, and any real score
+// exceeds the rescale threshold.  A state that saw no key keeps m = kEmptyMax,
+// l = 0, acc = 0; folds and merges weight it by 2^(kEmptyMax - M) = 0 (or, if
+// every state is empty, sum zeros and write 0).
+constexpr float kEmptyMax = -1e30f;
+
 // Online-softmax state for NCT 16-wide column tiles held by one wave.
 template <int D, int NCT>
 struct SoftmaxAcc {
   float m[NCT];     // reference max (log2 domain), identical across a column's 4 lanes
+  float thr[NCT];   // raw score above which m must move: (m + kRescaleSlack) / scale
   f32x4 lsum[NCT];  // [0]: the column's sum of P (an MFMA against ones: no lane reduction)
   f32x4 acc[NCT][Geo<D>::NT];
 
   __device__ __forceinline__ void init() {
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {
-      m[c] = kNegInf;
+      m[c] = kEmptyMax;
+      thr[c] = kEmptyMax;
       lsum[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int nt = 0; nt < Geo<D>::NT; ++nt) acc[c][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -194,12 +203,14 @@ constexpr float kRescaleSlack = 8.f;
 // skip the masking.
 //
 // The column tiles go in batches of up to kAttendBatch; a batch runs in
-// phases — its Q.K^T MFMAs, its columns' maxima, one (rare) reference-max
-// update with accumulator rescale, its exponentials, its P.V MFMAs and the
-// P.1 MFMA that accumulates the row sums — with no branch inside a phase, so
-// one wave overlaps a column tile's VALU work with the MFMAs of the others.
-// The max runs on raw scores (the scale is positive) and exp2 takes
-// fma(s, scale, -m).
+// phases — its Q.K^T MFMAs, each lane's maximum of its raw scores against the
+// column's threshold, one (rare) reference-max update with accumulator
+// rescale, its exponentials, its P.V MFMAs and the P.1 MFMA that accumulates
+// the row sums — with no branch inside a phase, so one wave overlaps a column
+// tile's VALU work with the MFMAs of the others.  The common step needs no
+// cross-lane column maximum: a lane compares its own maximum with the
+// threshold (the scale is positive), and only the rare update reduces the
+// column (col_max4).  exp2 takes fma(s, scale, -m).
 #ifndef CIE_ATTEND_BATCH
 #define CIE_ATTEND_BATCH 2
 #endif
@@ -254,7 +265,7 @@ __device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const K
       }
     }
     float sc[SB][8];
-    float mb[SB];
+    float xb[SB];  // the lane's maximum raw score per column tile
     bool need = false;
 #pragma unroll
     for (int i = 0; i < SB; ++i) {
@@ -274,10 +285,9 @@ __device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const K
             sc[i][4 + r] = kbb + r < lim[c] ? sc[i][4 + r] : kNegInf;
           }
         }
-        const float x = fmaxf(fmaxf(fmaxf(sc[i][0], sc[i][1]), fmaxf(sc[i][2], sc[i][3])),
-                              fmaxf(fmaxf(sc[i][4], sc[i][5]), fmaxf(sc[i][6], sc[i][7])));
-        mb[i] = col_max4(x) * scale_log2;
-        need |= mb[i] > st.m[c] + kRescaleSlack;
+        xb[i] = fmaxf(fmaxf(fmaxf(sc[i][0], sc[i][1]), fmaxf(sc[i][2], sc[i][3])),
+                      fmaxf(fmaxf(sc[i][4], sc[i][5]), fmaxf(sc[i][6], sc[i][7])));
+        need |= xb[i] > st.thr[c];
       }
     }
     if (__any(need)) {  // rare: move the reference max, rescale the state
@@ -285,10 +295,10 @@ __device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const K
       for (int i = 0; i < SB; ++i) {
         if (c0 + i < NCT) {
           const int c = c0 + i;
-          const float m_new = fmaxf(st.m[c], mb[i]);
-          // A column with every key masked so far keeps m = -inf, l = 0, acc = 0.
-          const float alpha = fast_exp2(st.m[c] - (m_new == kNegInf ? 0.f : m_new));
+          const float m_new = fmaxf(st.m[c], col_max4(xb[i]) * scale_log2);
+          const float alpha = fast_exp2(st.m[c] - m_new);  // 0 for an empty state
           st.m[c] = m_new;
+          st.thr[c] = (m_new + kRescaleSlack) / scale_log2;
           st.lsum[c][0] *= alpha;
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) st.acc[c][nt] *= alpha;
@@ -299,10 +309,9 @@ __device__ __forceinline__ void attend_pair_body(SoftmaxAcc<D, NCT>& st, const K
 #pragma unroll
     for (int i = 0; i < SB; ++i) {
       if (c0 + i < NCT) {
-        const float m_use = st.m[c0 + i] == kNegInf ? 0.f : st.m[c0 + i];
+        const float m = st.m[c0 + i];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          pop[i][e] = (f16)fast_exp2(__builtin_fmaf(sc[i][e], scale_log2, -m_use));
+        for (int e = 0; e < 8; ++e) pop[i][e] = (f16)fast_exp2(__builtin_fmaf(sc[i][e], scale_log2, -m));
       }
     }
 #pragma unroll

@@ -15,7 +15,8 @@
 // row of the tile inside the MFMA.  One work item is (tile, column group,
 // key chunk): a column group is up to col_group<D>() column tiles, and a
 // tile's key range [0, kv_len + last row + 1) is cut into chunks only when it
-// is longer than kWavePairs 32-key steps per wave.  The item's key tiles are
+// is longer than kWavePairs 32-key steps per wave (CIE_MIXED_NARROW_PAIRS for
+// a tile of one column tile, e.g. a decode row).  The item's key tiles are
 // split over the workgroup's waves; every wave carries all of the group's
 // column tiles, so each K/V byte is loaded once per workgroup and reused by
 // every column of the group in registers.  The waves fold their states
@@ -35,6 +36,10 @@ namespace cie {
 //   CIE_MIXED_CG           column tiles per work item (D = 64)
 //   CIE_MIXED_WAVE_PAIRS   32-key steps per wave before a tile's keys are
 //                          split over several workgroups
+//   CIE_MIXED_NARROW_PAIRS the same for a tile of one column tile (a decode
+//                          row: its steps are cheap, its keys many, so it is
+//                          split sooner and its chunks spread over idle
+//                          workgroups)
 //   CIE_MIXED_PF           32-key steps of loads in flight per wave (D = 64)
 //   CIE_MIXED_QLDS         1: the item's Q operands live in LDS, not registers
 //                          (a wave then fits 256 registers at D = 64)
@@ -56,6 +61,9 @@ namespace cie {
 #endif
 #ifndef CIE_MIXED_WG_PER_CU
 #define CIE_MIXED_WG_PER_CU 1
+#endif
+#ifndef CIE_MIXED_NARROW_PAIRS
+#define CIE_MIXED_NARROW_PAIRS 8
 #endif
 
 constexpr int kWavePairs = CIE_MIXED_WAVE_PAIRS;
@@ -141,7 +149,7 @@ __device__ __forceinline__ TilePlan tile_plan(int qt, const SeqInfo& s, int G, i
   t.key_end = s.c + t.row0 + t.rows;
   t.n_ktiles = (t.key_end + 15) >> 4;
   t.n_pairs = (t.n_ktiles + 1) >> 1;
-  const int per = waves * kWavePairs;
+  const int per = waves * (t.n_ctiles == 1 ? CIE_MIXED_NARROW_PAIRS : kWavePairs);
   t.n_chunks = max(1, min(kMaxChunks, (t.n_pairs + per - 1) / per));
   return t;
 }
