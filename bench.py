@@ -39,8 +39,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 # HBM bytes per launch of the measured kernel, from rocprofv3 FETCH_SIZE x 2.0 +
 # WRITE_SIZE (scale factors from a plain 256 MiB copy), committed under profiles/
 TRAFFIC_BYTES = {
-    2: (69_720_371, "profiles/hbm_traffic_decode_config2.md"),
-    3: (48_401_203, "profiles/mixed_attention_config3.md"),
+    2: (69_710_029, "profiles/hbm_traffic_decode_config2.md"),
+    3: (49_064_243, "profiles/mixed_attention_config3.md"),
 }
 HBM_PEAK_GBPS = 8000.0
 MIN_ROTATION_BYTES = 512 << 20
@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of graph replay")
     ap.add_argument("--copy-calib", action="store_true")
+    ap.add_argument("--probe-sweep", action="store_true",
+                    help="gather-probe rate by read volume and chunk size (the paged-read ceiling)")
     ap.add_argument("--repeats", type=int, default=5)
     return ap.parse_args()
 
@@ -152,14 +154,15 @@ def cpu_baseline(case, budget_s: float = 20.0, max_runs: int = 7):
     return statistics.median(runs) * 1e6, len(runs), torch.get_num_threads(), out
 
 
-def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chunk: int = 2048):
+def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chunk: int = 2048,
+                   region_bytes: int = 1 << 30):
     """HBM ceiling of the paged access pattern on this box: the probe kernel reads
     the same byte volume as one decode call as shuffled chunk-sized pieces of a
     1 GiB region (R disjoint chunk lists rotate, so the 256 MB MALL cannot help)."""
     from custom_inference_engine_amd import _native
 
     lib = _native.load()
-    region = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    region = torch.ones(region_bytes, dtype=torch.uint8, device=dev)
     n_region = region.numel() // chunk
     n = nbytes // chunk
     R = max(1, min(8, n_region // n))
@@ -200,6 +203,23 @@ def copy_calibration(args):
     print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
 
 
+def probe_sweep(args):
+    """The gather probe's time per launch by read volume (2 KiB chunks) and by chunk
+    size (64 MB): separates its fixed cost from the DRAM rate of shuffled chunks.
+    Volumes whose R rotating lists fit in the 256 MB MALL are marked cache-resident."""
+    dev = torch.device("cuda:0")
+    region = 2 << 30
+    cases = [(mb << 20, 2048) for mb in (8, 16, 32, 64, 128, 256, 512)]
+    cases += [(64 << 20, 1024), (64 << 20, 4096)]
+    for nbytes, chunk in cases:
+        R = max(1, min(8, (region // chunk) // (nbytes // chunk)))
+        steps = 64 if nbytes >= 256 << 20 else 200
+        us, moved = gather_ceiling(dev, nbytes, steps, 16, 3, chunk, region)
+        print(json.dumps({"probe_bytes": moved, "chunk": chunk, "rotation": R, "us": round(us, 2),
+                          "TBps": round(moved / us / 1e6, 3), "cache_resident": R * moved <= 256 << 20}),
+              flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -211,6 +231,8 @@ def main():
         sys.exit(2)
     if args.copy_calib:
         return copy_calibration(args)
+    if args.probe_sweep:
+        return probe_sweep(args)
 
     import custom_inference_engine_amd as cie
     from custom_inference_engine_amd import _native
@@ -405,6 +427,16 @@ def bench_mixed(args, cie, inputs, ref, dev):
     log(f"mixed parity: max abs err {err:.2e}")
     us, steps = time_calls([call(i) for i in range(R)], args.steps, args.warmup, not args.no_graph,
                            args.repeats)
+
+    # the mixed kernel alone (the roofline's kernel), on the same rotating layers
+    def mixed_only(i):
+        L = layers[i]
+        return lambda: cie.mixed_gqa_attention(L.q, L.kp, L.vp, 256, c.cu_seqlens, c.kv_lens, c.slot_ids,
+                                               c.block_table)
+
+    us_mix, _ = time_calls([mixed_only(i) for i in range(R)], args.steps, args.warmup, not args.no_graph,
+                           args.repeats)
+    log(f"config 3: {us:.2f} us/call (append + mixed), mixed kernel alone {us_mix:.2f} us/launch")
     E = (case.kv_lens + case.new_lens).tolist()
     kv_bytes = 2 * sum(E) * 2 * 64 * 2
     qo = 2 * case.T * 14 * 64 * 2
@@ -420,13 +452,14 @@ def bench_mixed(args, cie, inputs, ref, dev):
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6),
         "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
         "achieved_TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
+        "us_mixed_kernel": round(us_mix, 3),
         "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
         "config": {"workload": "config 3 mixed: 4x256-row prefill chunks + 28 decode rows", "T": case.T,
                    "algorithmic_bytes": nbytes, "flops": flops, "layer_rotation": R},
-        "roofline": {"bound": "mfma", "kernel": "mixed_attention_kernel<64> (+ kv_append_kernel<8,false>)",
-                     "achieved": round(flops / (us * 1e-6) / 1e12, 2), "peak": MFMA_F16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(flops / (us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                     "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "mfma", "kernel": "mixed_attention_kernel<64>",
+                     "achieved": round(flops / (us_mix * 1e-6) / 1e12, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flops / (us_mix * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                     "hbm_frac": round((nbytes - app) / (us_mix * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
                      "traffic": TRAFFIC_BYTES[3][0], "traffic_source": TRAFFIC_BYTES[3][1]},
         "parity_max_abs_err": err,
     }), flush=True)

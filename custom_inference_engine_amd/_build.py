@@ -3,6 +3,10 @@
 The library is compiled straight from ``csrc/*.hip`` for gfx950 only; the built
 ``.so`` sits next to this file so it travels with the source tree.  Objects go
 to ``_build/`` and the final link replaces the library atomically.
+
+Tuning variants (the kernels' ``CIE_*`` build-time settings) build elsewhere:
+``python -m custom_inference_engine_amd._build -D CIE_MIXED_NARROW_PAIRS=6 --out DIR``
+writes ``DIR/libcie_paged.so``, which the loader takes from ``CIE_PAGED_LIB``.
 """
 from __future__ import annotations
 
@@ -31,8 +35,8 @@ HIPCC_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # no kernel produces NaN (masked scores are -inf, and -inf - -inf is
-    # guarded): lets max trees use v_max3 without canonicalizing moves
+    # no kernel produces NaN (masked scores are -inf and the running max is
+    # always finite): lets max trees use v_max3 without canonicalizing moves
     "-fno-honor-nans",
     "-munsafe-fp-atomics",
 ]
@@ -45,9 +49,9 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: str, verbose: bool) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
+def _compile(src: str, verbose: bool, obj_dir: str = BUILD_DIR, defines: tuple = ()) -> str:
+    obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), "-I", INCLUDE, "-I", CSRC, "-c",
            os.path.join(CSRC, src), "-o", obj, "-Rpass-analysis=kernel-resource-usage"]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -68,21 +72,34 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source for gfx950 and link ``libcie_paged.so``."""
-    os.makedirs(BUILD_DIR, exist_ok=True)
+def build(verbose: bool = False, defines: tuple = (), out_dir: str | None = None) -> str:
+    """Compile every HIP source for gfx950 and link ``libcie_paged.so`` (in-tree, or a
+    tuning variant with extra ``NAME=VALUE`` defines into ``out_dir``)."""
+    if (defines or out_dir) and not out_dir:
+        raise ValueError("a build with extra defines needs its own out_dir")
+    obj_dir = os.path.join(out_dir, "_build") if out_dir else BUILD_DIR
+    lib_path = os.path.join(out_dir, LIB_NAME) if out_dir else LIB_PATH
+    os.makedirs(obj_dir, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
-    tmp = LIB_PATH + ".tmp"
+        objs = list(ex.map(lambda s: _compile(s, verbose, obj_dir, tuple(defines)), SOURCES))
+    tmp = lib_path + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib_path)
+    return lib_path
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    import argparse
+
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("-v", action="store_true", help="print the compiler commands")
+    ap.add_argument("-D", dest="defines", action="append", default=[], metavar="NAME=VALUE",
+                    help="a CIE_* build setting (variant builds need --out)")
+    ap.add_argument("--out", default=None, help="directory of a variant build")
+    a = ap.parse_args()
+    print(build(verbose=a.v, defines=tuple(a.defines), out_dir=a.out))
