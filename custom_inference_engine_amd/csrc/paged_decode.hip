@@ -282,13 +282,47 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
     return (int)page;
   };
   constexpr int kSpecTiles = 16;
-  int pages = lane < kSpecTiles ? lane_page(lane) : 0;
+  // Every load of the start goes out before any check: a check's error store
+  // (set_err) may alias later loads as far as the compiler knows, so a check
+  // placed between two loads makes the second wait for the first's data.
+  // Issued together, the first tiles' page ids, the length and Q take one
+  // memory round trip.
+  const int t_spec = gw + lane * TW;
+  const int64_t page_spec = (lane < kSpecTiles && t_spec < row_tiles) ? bt_row[t_spec / tpp] : 0;
+  const int64_t len_raw = kAppend ? p.lens[slot] : p.lens[b];
+  // Q^T operand: column r16 = head g*G + r16 (zero past the group).
+  f16x8 qop[1][KS];
+  const f16* qrow = p.q + (int64_t)b * p.q_row_stride + (int64_t)(g * p.G + r16) * D + 8 * grp;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    qop[0][ks] = (r16 < p.G) ? *reinterpret_cast<const f16x8*>(qrow + 32 * ks) : f16x8{};
+  f16x8 cs[KS], sn[KS], knew[KS];
+  if constexpr (kRope) {
+    const f16* crow = p.cos + (int64_t)b * p.cs_stride + 8 * grp;
+    const f16* srow = p.sin + (int64_t)b * p.cs_stride + 8 * grp;
+    const f16* krow = p.k_new + (int64_t)b * p.k_tok_stride + (int64_t)g * p.k_head_stride + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      cs[ks] = *reinterpret_cast<const f16x8*>(crow + 32 * ks);
+      sn[ks] = *reinterpret_cast<const f16x8*>(srow + 32 * ks);
+      knew[ks] = *reinterpret_cast<const f16x8*>(krow + 32 * ks);
+    }
+  }
 
+  int pages = 0;
+  if (lane < kSpecTiles && t_spec < row_tiles) {
+    int64_t page = page_spec;
+    if (page < 0 || page >= p.n_pages) {
+      set_err(p.err, CIE_ERRBIT_PAGE);
+      page = 0;
+    }
+    pages = (int)page;
+  }
   int L, pos = -1;
   {
     const int64_t cap = (int64_t)row_tiles * 16;
     if constexpr (kAppend) {
-      const int64_t prior = p.lens[slot];
+      const int64_t prior = len_raw;
       if (!slot_ok || prior < 0 || prior + 1 > cap) {
         if (slot_ok) set_err(p.err, CIE_ERRBIT_LEN);
         L = 0;
@@ -297,7 +331,7 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
         L = pos + 1;
       }
     } else {
-      int64_t len = p.lens[b];
+      int64_t len = len_raw;
       if (len < 0 || len > cap) {
         set_err(p.err, CIE_ERRBIT_LEN);
         len = len < 0 ? 0 : cap;
@@ -308,13 +342,6 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   const int n_tiles = (L + 15) >> 4;
   const int n_mine = n_tiles > gw ? (n_tiles - gw + TW - 1) / TW : 0;
 
-  // Q^T operand: column r16 = head g*G + r16 (zero past the group).
-  f16x8 qop[1][KS];
-  const f16* qrow = p.q + (int64_t)b * p.q_row_stride + (int64_t)(g * p.G + r16) * D + 8 * grp;
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-    qop[0][ks] = (r16 < p.G) ? *reinterpret_cast<const f16x8*>(qrow + 32 * ks) : f16x8{};
-
   const PagedSrc src{p.k_pool,  p.v_pool,  bt_row, (int64_t)g * p.pool_head_stride,
                      p.pool_page_stride, p.n_pages, p.page_size, p.err};
   NewRow<D> nr{nullptr, nullptr, -1};
@@ -323,19 +350,10 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
     nr.v = p.v_new + (int64_t)b * p.v_tok_stride + (int64_t)g * p.v_head_stride;
     nr.pos = pos;
   }
-  // Rope mode: rotate q now, and the new token's K row (every lane its dims)
-  // for the lanes of that key to take once its tile is loaded.
-  f16x8 knew[KS];
+  // Rope mode: rotate q now, and the new token's K row (every lane its dims,
+  // loaded with the start's other loads) for the lanes of that key to take
+  // once its tile is loaded.
   if constexpr (kRope) {
-    f16x8 cs[KS], sn[KS];
-    const f16* crow = p.cos + (int64_t)b * p.cs_stride + 8 * grp;
-    const f16* srow = p.sin + (int64_t)b * p.cs_stride + 8 * grp;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      cs[ks] = *reinterpret_cast<const f16x8*>(crow + 32 * ks);
-      sn[ks] = *reinterpret_cast<const f16x8*>(srow + 32 * ks);
-      knew[ks] = *reinterpret_cast<const f16x8*>(nr.k + 8 * grp + 32 * ks);
-    }
     rope_lane<D>(qop[0], cs, sn);
     rope_lane<D>(knew, cs, sn);
   }
