@@ -62,6 +62,8 @@ def test_mixed_shapes(native_lib, prior, new):
 @pytest.mark.parametrize("prior,new,d", [
     ([16000, 5], [20, 1], 64),       # a prefix long enough to split over several workgroups
     ([5000, 3000], [1, 33], 128),
+    ([30000], [1], 64),               # one decode row past the chunk cap (16 chunks of its keys)
+    ([30000, 9, 700], [1, 1, 1], 128),
 ], ids=lambda x: str(x))
 def test_mixed_long_prefixes_split_keys(native_lib, prior, new, d):
     case = inputs.make_case(prior, new, seed=37, d=d)
@@ -165,7 +167,7 @@ def test_mixed_rows_beyond_max_seqlen_are_flagged(native_lib):
 
 def test_mixed_counters_return_to_zero(native_lib):
     """Multi-chunk tiles (long prefixes) leave their arrival counters zero."""
-    case = inputs.make_case([6000, 0, 2500, 700], [40, 1, 1, 18], seed=36)
+    case = inputs.make_case([6000, 0, 2500, 700, 30000], [40, 1, 1, 18, 1], seed=36)
     note("mixed counters")
     c = case.to(DEV)
     kp, vp = (t.to(DEV) for t in case.appended_pools())
