@@ -343,8 +343,8 @@ def main():
     wl = ("paged GQA decode call = KV append + split-KV load + merge, one layer, one launch" if args.config == 2
           else "long-context paged GQA decode call (config 4)")
     n_splits = splits or cie.attn.core.default_decode_splits(case.B, 2, dev)
-    # the library runs half-size (4-wave) workgroups when the grid exceeds one per CU
-    waves = 8 if n_splits * 2 * case.B <= torch.cuda.get_device_properties(dev).multi_processor_count else 4
+    # the library's decode workgroups have 4 waves (one per SIMD) at D = 64
+    waves = 4
     line = {
         "metric": METRIC if args.config == 2 else
         "long-context paged GQA decode us/call + HBM GB/s (% of peak) at B=16 kv_len=16384 (config 4)",

@@ -70,10 +70,11 @@ __device__ __forceinline__ TileLoc tile_loc(const int64_t* __restrict__ bt_row, 
   return TileLoc{page * page_stride + head_off + (int64_t)off * D};
 }
 
-// Loads of a step's two tiles.  Both tiles are always loaded (a caller with
-// only one tile passes it twice and masks the copy with key kNoKey), so every
-// step issues the same loads and the compiler can wait for exactly the
-// oldest step in flight instead of draining all loads.
+// Loads of a step's two tiles (V rows non-temporal: a call reads each once).
+// Both tiles are always loaded (a caller with only one tile passes it twice
+// and masks the copy with key kNoKey), so every step issues the same loads
+// and the compiler can wait for exactly the oldest step in flight instead of
+// draining all loads.
 template <int D>
 __device__ __forceinline__ void load_pair(KVPair<D>& kv, const f16* __restrict__ kpool,
                                           const f16* __restrict__ vpool, TileLoc t0,
@@ -88,11 +89,11 @@ __device__ __forceinline__ void load_pair(KVPair<D>& kv, const f16* __restrict__
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) kv.k[0][ks] = *reinterpret_cast<const f16x8*>(k0 + 32 * ks);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) kv.v[e] = *reinterpret_cast<const vrow_t*>(v0 + e * D);
+  for (int e = 0; e < 4; ++e) kv.v[e] = stream_load(reinterpret_cast<const vrow_t*>(v0 + e * D));
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) kv.k[1][ks] = *reinterpret_cast<const f16x8*>(k1 + 32 * ks);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) kv.v[4 + e] = *reinterpret_cast<const vrow_t*>(v1 + e * D);
+  for (int e = 0; e < 4; ++e) kv.v[4 + e] = stream_load(reinterpret_cast<const vrow_t*>(v1 + e * D));
 }
 
 // A 16-key tile as a raw buffer: descriptor base = the tile's first row

@@ -79,6 +79,19 @@ __device__ __forceinline__ void rope8(f16x8& lo, f16x8& hi, f16x8 c_lo, f16x8 c_
   }
 }
 
+// A load of whole cache lines the kernel reads exactly once (V rows streamed
+// by the decode): the non-temporal policy (global_load ... nt) keeps them
+// from being allocated for reuse in the caches, which raises the HBM read
+// rate of shuffled 2 KiB pages from ~5.8 to ~6.5 TB/s on MI355X.  Not for
+// partial lines whose other part a later load reads: an operand-layout K
+// load covers half of each 128-byte row and the next k-step the other half,
+// and with nt that second half is fetched from HBM again (+4.5 % traffic and
+// +0.5 us per decode call when K was loaded this way).
+template <class T>
+__device__ __forceinline__ T stream_load(const T* p) {
+  return __builtin_nontemporal_load(p);
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

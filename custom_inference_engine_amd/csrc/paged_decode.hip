@@ -39,7 +39,7 @@
 //                     (sc1) partial stores / loads, 1 = last-arriver with
 //                     release / acquire fences, 3 = a second merge launch
 #ifndef CIE_DECODE_WAVES
-#define CIE_DECODE_WAVES 8
+#define CIE_DECODE_WAVES 4
 #endif
 #ifndef CIE_DECODE_PF
 #define CIE_DECODE_PF 1
@@ -84,7 +84,8 @@ struct NewRow {
   int pos;       // absolute key index of the new token (-1: none)
 };
 
-// Loads of one 16-key tile; the lanes holding key nr.pos read the new rows.
+// Loads of one 16-key tile (V rows non-temporal, as load_pair); the lanes
+// holding key nr.pos read the new rows.
 template <int D>
 __device__ __forceinline__ void load_tile_new(f16x8 (&k)[Geo<D>::KS],
                                               typename HVec<Geo<D>::NT>::type (&v)[4],
@@ -100,7 +101,7 @@ __device__ __forceinline__ void load_tile_new(f16x8 (&k)[Geo<D>::KS],
   for (int e = 0; e < 4; ++e) {
     const int row = 4 * grp + e;
     const f16* vp = (kt0 + row == nr.pos) ? nr.v + NT * r16 : src.v_pool + tl.base + row * D + NT * r16;
-    v[e] = *reinterpret_cast<const vrow_t*>(vp);
+    v[e] = stream_load(reinterpret_cast<const vrow_t*>(vp));
   }
 }
 
@@ -624,12 +625,14 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
   merge_splits<D, 256>(p, blockIdx.y, blockIdx.x);
 }
 
-// Waves per workgroup: a workgroup of decode_waves<D>() waves fills a CU's
-// wave slots at this kernel's register use (two waves per SIMD at D = 64; one
-// at D = 128, which needs twice the registers), so one workgroup per CU runs
-// at a time.  A grid with more workgroups than CUs would then run in rounds,
-// and the last round's stragglers set the call's time; such grids use
-// workgroups of half the waves instead, two per CU, all resident at once.
+// Waves per workgroup: four, one per SIMD.  With the non-temporal K/V loads
+// a 4-wave workgroup per CU streams faster than an 8-wave one (config 2:
+// 16.99 vs 18.08 us per call): the second wave per SIMD only queued more
+// loads behind the first's and doubled the fold.  At D = 64 the kernel fits
+// two waves per SIMD, so a grid of more workgroups than CUs (config 4: 512)
+// is still resident in one round, two workgroups per CU.  D = 128 needs twice
+// the registers (one wave per SIMD).  Variant builds with more waves halve
+// them for such grids, so those also stay resident in one round.
 template <int D>
 constexpr int decode_waves() {
   return D <= 64 ? CIE_DECODE_WAVES : (CIE_DECODE_WAVES > 4 ? 4 : CIE_DECODE_WAVES);

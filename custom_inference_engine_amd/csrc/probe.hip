@@ -1,9 +1,10 @@
 // Measurement helper: the HBM read ceiling for a paged access pattern.
 //
 // Reads n_chunks chunks of chunk_bytes each (chunk i at base + ids[i] *
-// chunk_bytes), 16 bytes per lane per load, four chunks in flight per
-// wavefront, and folds the data into one word so the loads cannot be
-// removed.  With the chunk size of a KV page-head (2 KiB) and shuffled ids it
+// chunk_bytes), 16 bytes per lane per non-temporal load (the decode's KV
+// load policy, and the fastest one measured for this pattern), four chunks
+// in flight per wavefront, and folds the data into one word so the loads
+// cannot be removed.  With the chunk size of a KV page-head (2 KiB) and shuffled ids it
 // is the paged decode's memory traffic without any of its math, i.e. the
 // attainable bandwidth the decode kernel is judged against.
 #include "cie_common.h"
@@ -26,7 +27,7 @@ __global__ __launch_bounds__(256) void gather_read_kernel(const u32x4* __restric
       const int64_t id = (c + j < n_chunks) ? ids[c + j] : ids[c];
       const u32x4* p = base + id * CHUNK16;
 #pragma unroll
-      for (int k = 0; k < PER_LANE; ++k) v[j][k] = p[k * kWave + lane];
+      for (int k = 0; k < PER_LANE; ++k) v[j][k] = stream_load(p + k * kWave + lane);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
