@@ -85,7 +85,12 @@ struct NewRow {
 };
 
 // Loads of one 16-key tile (V rows non-temporal, as load_pair); the lanes
-// holding key nr.pos read the new rows.
+// holding key nr.pos read the new rows.  Keys past nr.pos lie beyond the
+// sequence (the new token is its last key), so their lanes read the new rows
+// too instead of pool rows that would be masked anyway: a tail tile costs no
+// HBM traffic beyond its valid rows (at 4097 attended keys the last tile
+// holds the new token alone, and its wave would otherwise stream a whole
+// extra tile).  With nr.pos < 0 (no append) every lane reads the pool.
 template <int D>
 __device__ __forceinline__ void load_tile_new(f16x8 (&k)[Geo<D>::KS],
                                               typename HVec<Geo<D>::NT>::type (&v)[4],
@@ -94,13 +99,14 @@ __device__ __forceinline__ void load_tile_new(f16x8 (&k)[Geo<D>::KS],
   constexpr int KS = Geo<D>::KS;
   constexpr int NT = Geo<D>::NT;
   typedef typename HVec<NT>::type vrow_t;
-  const f16* kp = (kt0 + r16 == nr.pos) ? nr.k + 8 * grp : src.k_pool + tl.base + r16 * D + 8 * grp;
+  auto past = [&](int row) { return nr.pos >= 0 && kt0 + row >= nr.pos; };
+  const f16* kp = past(r16) ? nr.k + 8 * grp : src.k_pool + tl.base + r16 * D + 8 * grp;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) k[ks] = *reinterpret_cast<const f16x8*>(kp + 32 * ks);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int row = 4 * grp + e;
-    const f16* vp = (kt0 + row == nr.pos) ? nr.v + NT * r16 : src.v_pool + tl.base + row * D + NT * r16;
+    const f16* vp = past(row) ? nr.v + NT * r16 : src.v_pool + tl.base + row * D + NT * r16;
     v[e] = stream_load(reinterpret_cast<const vrow_t*>(vp));
   }
 }
