@@ -138,19 +138,26 @@ struct TilePlan {
   int row0, rows, n_combos, n_ctiles, n_groups, key_end, n_ktiles, n_pairs, n_chunks;
 };
 
-// cg = column tiles per group, waves = wavefronts per workgroup.
-__device__ __forceinline__ TilePlan tile_plan(int qt, const SeqInfo& s, int G, int cg, int waves) {
+// CG = column tiles per group, W = wavefronts per workgroup (template
+// arguments, so the chunk count divides by constants: a work item's lookup
+// walks its sequence's tiles, and a run-time division per tile cost ~2 us on
+// the last tiles of a 2,304-key sequence).
+template <int CG, int W>
+__device__ __forceinline__ TilePlan tile_plan(int qt, const SeqInfo& s, int G) {
   TilePlan t;
   t.row0 = qt * 16;
   t.rows = min(16, s.L - t.row0);
   t.n_combos = t.rows * G;
   t.n_ctiles = (t.n_combos + 15) >> 4;
-  t.n_groups = (t.n_ctiles + cg - 1) / cg;
+  t.n_groups = (t.n_ctiles + CG - 1) / CG;
   t.key_end = s.c + t.row0 + t.rows;
   t.n_ktiles = (t.key_end + 15) >> 4;
   t.n_pairs = (t.n_ktiles + 1) >> 1;
-  const int per = waves * (t.n_ctiles == 1 ? CIE_MIXED_NARROW_PAIRS : kWavePairs);
-  t.n_chunks = max(1, min(kMaxChunks, (t.n_pairs + per - 1) / per));
+  constexpr int kPerNarrow = W * CIE_MIXED_NARROW_PAIRS;
+  constexpr int kPerWide = W * kWavePairs;
+  const int chunks = t.n_ctiles == 1 ? (t.n_pairs + kPerNarrow - 1) / kPerNarrow
+                                     : (t.n_pairs + kPerWide - 1) / kPerWide;
+  t.n_chunks = max(1, min(kMaxChunks, chunks));
   return t;
 }
 
@@ -381,11 +388,12 @@ constexpr int kMaxSeqs = 1024;  // sequences a launch can plan (LDS prefix table
 
 // Items of sequence s: sum over its (grid-covered) query tiles of
 // column groups x chunks.
-__device__ __forceinline__ int seq_items(const SeqInfo& s, int n_qtiles, int G, int cg, int waves) {
+template <int CG, int W>
+__device__ __forceinline__ int seq_items(const SeqInfo& s, int n_qtiles, int G) {
   const int n_tiles = min((s.L + 15) >> 4, n_qtiles);
   int n = 0;
   for (int qt = 0; qt < n_tiles; ++qt) {
-    const TilePlan tp = tile_plan(qt, s, G, cg, waves);
+    const TilePlan tp = tile_plan<CG, W>(qt, s, G);
     n += tp.n_groups * tp.n_chunks;
   }
   return n;
@@ -404,7 +412,7 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   const int wave = uniform(threadIdx.x / kWave);
   const int r16 = lane & 15;
   const int grp = lane >> 4;
-  const TilePlan tp = tile_plan(qt, s, p.G, CG, W);
+  const TilePlan tp = tile_plan<CG, W>(qt, s, p.G);
   const int gi = j / tp.n_chunks;
   const int chunk = j - gi * tp.n_chunks;
   const int ct0 = gi * CG;
@@ -495,7 +503,7 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
       sm_prior[b] = s.c;
       if (g == 0 && blockIdx.x == 0 && ((s.L + 15) >> 4) > p.n_qtiles)
         set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
-      n = s.L > 0 ? seq_items(s, p.n_qtiles, p.G, CG, W) : 0;
+      n = s.L > 0 ? seq_items<CG, W>(s, p.n_qtiles, p.G) : 0;
     }
     // inclusive block scan of n over this pass's span of sequences
     const int span = min(NTH, p.B - b0);
@@ -536,7 +544,7 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     int j = item - uniform(sm_prefix[b]);
     int qt = 0;
     for (;; ++qt) {
-      const TilePlan tp = tile_plan(qt, s, p.G, CG, W);
+      const TilePlan tp = tile_plan<CG, W>(qt, s, p.G);
       const int nt = tp.n_groups * tp.n_chunks;
       if (j < nt) break;
       j -= nt;
