@@ -543,6 +543,18 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     s.c = uniform(sm_prior[b]);
     int j = item - uniform(sm_prefix[b]);
     int qt = 0;
+    // Full (16-row) tiles all have the same column groups, and their chunk
+    // count grows with the tile index; if the last full tile is one chunk,
+    // every full tile is n_groups items and the item's tile is a division.
+    // Otherwise (and for the partial last tile) walk the tiles.
+    const int n_full = min(s.L >> 4, p.n_qtiles);
+    if (n_full > 0) {
+      const TilePlan lf = tile_plan<CG, W>(n_full - 1, s, p.G);
+      if (lf.n_chunks == 1) {
+        qt = min(j / lf.n_groups, n_full);
+        j -= qt * lf.n_groups;
+      }
+    }
     for (;; ++qt) {
       const TilePlan tp = tile_plan<CG, W>(qt, s, p.G);
       const int nt = tp.n_groups * tp.n_chunks;
