@@ -41,8 +41,9 @@ namespace cie {
 //                          split sooner and its chunks spread over idle
 //                          workgroups)
 //   CIE_MIXED_PF           32-key steps of loads in flight per wave (D = 64)
-//   CIE_MIXED_QLDS         1: the item's Q operands live in LDS, not registers
-//                          (a wave then fits 256 registers at D = 64)
+//   CIE_MIXED_QLDS         1: the item's Q operands live in LDS (one copy per
+//                          workgroup), not registers (a wave then fits 256
+//                          registers at D = 64)
 //   CIE_MIXED_WG_PER_CU    workgroups per CU in the grid
 #ifndef CIE_MIXED_WAVES
 #define CIE_MIXED_WAVES 4
@@ -190,6 +191,13 @@ __device__ __forceinline__ void load_combo_q(const MixedParams& p, const SeqInfo
   }
 }
 
+// Key limit of column tile ct's lane column (load_combo_q's lim alone).
+__device__ __forceinline__ int combo_lim(const MixedParams& p, const SeqInfo& s,
+                                         const TilePlan& tp, int ct, int r16) {
+  const int cc = ct * 16 + r16;
+  return cc < tp.n_combos ? s.c + tp.row0 + cc / p.G + 1 : tp.key_end;
+}
+
 // Row of column cc of the tile relative to the tile's first row's first q
 // head, in units of (row, q head) = H_q * (row) + g * G + head - ...; i.e. the
 // index into [(t0 + row0) * H_q, ...) of the tile's partial / output rows.
@@ -248,28 +256,38 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
   constexpr int NT = Geo<D>::NT;
   constexpr int KS = Geo<D>::KS;
   constexpr int W = mixed_waves<D>();
-  f16x8 qop[NCT][KS];
-  int lim[NCT];
-#pragma unroll
-  for (int c = 0; c < NCT; ++c) load_combo_q<D>(p, s, tp, g, ct0 + c, r16, grp, qop[c], lim[c]);
   SoftmaxAcc<D, NCT> st;
   st.init();
   if constexpr (CIE_MIXED_QLDS) {
-    // this wave's block of Q operands in LDS (read back by this wave only),
-    // written while the wave's first page ids are in flight: the Q loads and
-    // the page-id loads then share one memory round trip
-    f16x8* mine = sm_q + wave * (col_group<D>() * KS * kWave);
+    // One copy of the item's Q operands per workgroup, in LDS: wave c loads
+    // column tile c (every wave streams keys against all of them), and the
+    // copy is written while each wave's first page ids are in flight, so the
+    // Q loads and the page-id loads share one memory round trip; a barrier
+    // then publishes it to every wave before the first step.
+    static_assert(col_group<D>() <= W, "one wave per column tile of a group");
+    int lim[NCT];
+    f16x8 qw[KS];
+    int lim_w;
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) lim[c] = combo_lim(p, s, tp, ct0 + c, r16);
+    const bool loads = wave < NCT;
+    if (loads) load_combo_q<D>(p, s, tp, g, ct0 + wave, r16, grp, qw, lim_w);
     const int lane = threadIdx.x & (kWave - 1);
     auto stage_q = [&]() {
+      if (loads) {
 #pragma unroll
-      for (int c = 0; c < NCT; ++c)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) mine[(c * KS + ks) * kWave + lane] = qop[c][ks];
+        for (int ks = 0; ks < KS; ++ks) sm_q[(wave * KS + ks) * kWave + lane] = qw[ks];
+      }
+      __syncthreads();
       MIXED_TRACE(item, 9, __builtin_amdgcn_s_memrealtime());
     };
-    stream_tiles<D, NCT, mixed_pf<D>()>(st, QLds<D>{mine, lane}, lim, w0, w1, tp.key_end, src,
+    stream_tiles<D, NCT, mixed_pf<D>()>(st, QLds<D>{sm_q, lane}, lim, w0, w1, tp.key_end, src,
                                         p.scale_log2, r16, grp, stage_q);
   } else {
+    f16x8 qop[NCT][KS];
+    int lim[NCT];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) load_combo_q<D>(p, s, tp, g, ct0 + c, r16, grp, qop[c], lim[c]);
     MIXED_TRACE(item, 9, __builtin_amdgcn_s_memrealtime());
     stream_tiles<D, NCT, mixed_pf<D>()>(st, QRegs<D, NCT>{qop}, lim, w0, w1, tp.key_end, src,
                                         p.scale_log2, r16, grp, [] {});
@@ -479,7 +497,7 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
   __shared__ float sm_m[W][16];
   __shared__ float sm_l[W][16];
   __shared__ __attribute__((aligned(16))) float sm_acc[W][16][D + 4];
-  __shared__ f16x8 sm_q[CIE_MIXED_QLDS ? W * col_group<D>() * Geo<D>::KS * kWave : 1];
+  __shared__ f16x8 sm_q[CIE_MIXED_QLDS ? col_group<D>() * Geo<D>::KS * kWave : 1];
   __shared__ int sm_last;
   __shared__ int sm_prefix[kMaxSeqs + 1];
   __shared__ int sm_scan[NTH];
