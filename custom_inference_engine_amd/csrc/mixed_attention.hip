@@ -70,6 +70,8 @@ namespace cie {
 constexpr int kWavePairs = CIE_MIXED_WAVE_PAIRS;
 constexpr int kMaxChunks = 16;    // workgroups per (tile, column group) at most
 constexpr int kMaxColGroups = 8;  // column groups per tile at most (<= 8 column tiles)
+constexpr int kFoldTiles = 2;     // column tiles whose wave states share one fold round
+
 
 // Wavefronts per workgroup, column tiles per work item (registers: 16*NT
 // accumulators each) and load prefetch depth (registers: one 32-key K/V step
@@ -85,6 +87,12 @@ constexpr int col_group() {
 template <int D>
 constexpr int mixed_pf() {
   return D <= 64 ? CIE_MIXED_PF : 1;
+}
+
+// Column tiles of one fold round at head dim D (a group may have fewer).
+template <int D>
+constexpr int fold_tiles() {
+  return col_group<D>() < kFoldTiles ? col_group<D>() : kFoldTiles;
 }
 
 struct MixedParams {
@@ -251,8 +259,7 @@ template <int D, int NCT>
 __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s,
                                           const TilePlan& tp, int g, int ct0, int chunk, int w0,
                                           int w1, const PagedSrc& src, int wave, int r16, int grp,
-                                          float (*sm_m)[16], float (*sm_l)[16],
-                                          float (*sm_acc)[16][D + 4], f16x8* sm_q, int item) {
+                                          f32x4* sm_facc, float2* sm_fml, f16x8* sm_q, int item) {
   constexpr int NT = Geo<D>::NT;
   constexpr int KS = Geo<D>::KS;
   constexpr int W = mixed_waves<D>();
@@ -293,53 +300,96 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
                                         p.scale_log2, r16, grp, [] {});
   }
   MIXED_TRACE(item, 8, __builtin_amdgcn_s_memrealtime());
+  // Fold the waves' states, kFoldTiles column tiles per round: every wave
+  // puts its states of the round's column tiles into LDS in its register
+  // layout, and after a barrier wave c combines column tile c lane by lane —
+  // each lane reads its own (column, dims) slots of the other waves' states,
+  // so the reads are conflict-free and the SIMDs fold their tiles at once —
+  // and writes o (single chunk) or the chunk's partial.  (Every column tile
+  // in one round needs 72 KB of LDS at D = 64; past ~72 KB per workgroup the
+  // kernel's loads slow down, measured: unused LDS up to 72 KB cost nothing,
+  // 109 KB cost 12 %.)
+  static_assert(NCT <= W, "a wave per column tile of the group");
+  constexpr int FT = fold_tiles<D>();
+  const int lane = threadIdx.x & (kWave - 1);
   const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
   const PartRegion pr = part_region<D>(p, s, tp);
 #pragma unroll
-  for (int c = 0; c < NCT; ++c) {
-    const float l = st.l(c);
-    __syncthreads();  // the previous column tile's fold has read the LDS
-    if (grp == 0) {
-      sm_m[wave][r16] = st.m[c];
-      sm_l[wave][r16] = l;
+  for (int c0 = 0; c0 < NCT; c0 += FT) {
+    if (c0 > 0) __syncthreads();  // the previous round's reads are done
+#pragma unroll
+    for (int c = c0; c < NCT && c < c0 + FT; ++c) {
+      if (c == wave) continue;  // wave c keeps its own state in registers
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        sm_facc[((wave * FT + c - c0) * NT + nt) * kWave + lane] = st.acc[c][nt];
+      sm_fml[(wave * FT + c - c0) * kWave + lane] = float2{st.m[c], st.l(c)};
     }
-    // lane (r16, grp) holds dims NT * (4 * grp + r) + nt: 4 * NT contiguous floats
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int nq = 0; nq < NT / 4; ++nq)
-        *reinterpret_cast<f32x4*>(&sm_acc[wave][r16][NT * (4 * grp + r) + 4 * nq]) =
-            f32x4{st.acc[c][4 * nq][r], st.acc[c][4 * nq + 1][r], st.acc[c][4 * nq + 2][r],
-                  st.acc[c][4 * nq + 3][r]};
     __syncthreads();
-    const int n_cols = min(16, tp.n_combos - (ct0 + c) * 16);
-    for (int it = threadIdx.x; it < n_cols * (D / 4); it += W * kWave) {
-      const int j = it / (D / 4);
-      const int d = (it - j * (D / 4)) * 4;
-      float M = kNegInf;
 #pragma unroll
-      for (int w = 0; w < W; ++w) M = fmaxf(M, sm_m[w][j]);
-      f32x4 num = {0.f, 0.f, 0.f, 0.f};
-      float den = 0.f;
+    for (int c = c0; c < NCT && c < c0 + FT; ++c) {
+      if (c != wave) continue;
+      float mw[W], lw[W];
 #pragma unroll
       for (int w = 0; w < W; ++w) {
-        const float mw = sm_m[w][j];
-        const float a = mw == kNegInf ? 0.f : fast_exp2(mw - M);
-        num += a * *reinterpret_cast<const f32x4*>(&sm_acc[w][j][d]);
-        den = __builtin_fmaf(a, sm_l[w][j], den);
+        if (w == c) {
+          mw[w] = st.m[c];
+          lw[w] = st.l(c);
+        } else {
+          const float2 ml = sm_fml[(w * FT + c - c0) * kWave + lane];
+          mw[w] = ml.x;
+          lw[w] = ml.y;
+        }
       }
-      const int off = column_off(p, g, (ct0 + c) * 16 + j);
-      if (tp.n_chunks == 1) {
-        const float inv = den > 0.f ? 1.f / den : 0.f;
-        const f16x4 h = {(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
-                         (f16)(num[3] * inv)};
-        *reinterpret_cast<f16x4*>(p.o + (tile_row0 + off) * D + d) = h;
-      } else {
-        const int prow = off * kMaxChunks + chunk;
-        agent_store4(pr.acc, (uint32_t)((prow * D + d) * sizeof(float)), num);
-        if (d == 0) {
-          agent_store(pr.m + prow, M);
-          agent_store(pr.l + prow, den);
+      float M = mw[0];
+#pragma unroll
+      for (int w = 1; w < W; ++w) M = fmaxf(M, mw[w]);
+      // a state that saw no key holds kEmptyMax and weighs 2^(kEmptyMax - M)
+      // = 0 (if every state is empty, M = kEmptyMax: den = 0 and o = 0)
+      f32x4 num[NT];
+      float den = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) num[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float a = fast_exp2(mw[w] - M);
+        den = __builtin_fmaf(a, lw[w], den);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          num[nt] += a * (w == c ? st.acc[c][nt]
+                                 : sm_facc[((w * FT + c - c0) * NT + nt) * kWave + lane]);
+      }
+      const int n_cols = min(16, tp.n_combos - (ct0 + c) * 16);
+      if (r16 < n_cols) {
+        // lane (r16, grp) holds dims NT * (4 * grp + r) + nt: 4 * NT
+        // contiguous dims from 4 * NT * grp of column r16
+        const int off = column_off(p, g, (ct0 + c) * 16 + r16);
+        const int d0 = 4 * NT * grp;
+        if (tp.n_chunks == 1) {
+          const float inv = den > 0.f ? 1.f / den : 0.f;
+#pragma unroll
+          for (int h = 0; h < NT / 2; ++h) {  // 8 dims per 16-byte store
+            f16x8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int k = 8 * h + e;  // dim d0 + k = d0 + NT * r + nt
+              v[e] = (f16)(num[k % NT][k / NT] * inv);
+            }
+            *reinterpret_cast<f16x8*>(p.o + (tile_row0 + off) * D + d0 + 8 * h) = v;
+          }
+        } else {
+          const int prow = off * kMaxChunks + chunk;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int nq = 0; nq < NT / 4; ++nq)
+              agent_store4(pr.acc, (uint32_t)((prow * D + d0 + NT * r + 4 * nq) * sizeof(float)),
+                           f32x4{num[4 * nq][r], num[4 * nq + 1][r], num[4 * nq + 2][r],
+                                 num[4 * nq + 3][r]});
+          if (grp == 0) {
+            agent_store(pr.m + prow, M);
+            agent_store(pr.l + prow, den);
+          }
         }
       }
     }
@@ -402,7 +452,13 @@ __device__ __forceinline__ void merge_group(const MixedParams& p, const SeqInfo&
   }
 }
 
-constexpr int kMaxSeqs = 1024;  // sequences a launch can plan (LDS prefix table)
+constexpr int kMaxSeqs = 1024;  // sequences a launch can plan (LDS plan tables)
+
+// Bytes of the kernel's dynamic LDS: the plan tables of B sequences (t0 as
+// int64, slot / rows / prior / item prefix as int32).
+static size_t mixed_plan_lds(int B) {
+  return (size_t)B * sizeof(int64_t) + (size_t)(4 * B + 1) * sizeof(int);
+}
 
 // Items of sequence s: sum over its (grid-covered) query tiles of
 // column groups x chunks.
@@ -421,8 +477,8 @@ __device__ __forceinline__ int seq_items(const SeqInfo& s, int n_qtiles, int G) 
 // b, kv head g.
 template <int D>
 __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo& s, int b, int g,
-                                             int qt, int j, float (*sm_m)[16], float (*sm_l)[16],
-                                             float (*sm_acc)[16][D + 4], f16x8* sm_q, int* sm_last,
+                                             int qt, int j, f32x4* sm_facc, float2* sm_fml,
+                                             f16x8* sm_q, int* sm_last,
                                              int item) {
   constexpr int CG = col_group<D>();
   constexpr int W = mixed_waves<D>();
@@ -446,7 +502,7 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
 #define CIE_GROUP_CASE(k)                                                                      \
   case k:                                                                                      \
     if constexpr (k <= CG)                                                                     \
-      run_group<D, k>(p, s, tp, g, ct0, chunk, w0, w1, src, wave, r16, grp, sm_m, sm_l, sm_acc, \
+      run_group<D, k>(p, s, tp, g, ct0, chunk, w0, w1, src, wave, r16, grp, sm_facc, sm_fml, \
                       sm_q, item);                                                             \
     break;
     CIE_GROUP_CASE(1)
@@ -494,17 +550,23 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
   static_assert(col_group<D>() <= 4 && 8 / col_group<D>() <= kMaxColGroups, "column groups");
   constexpr int W = mixed_waves<D>();
   constexpr int NTH = W * kWave;
-  __shared__ float sm_m[W][16];
-  __shared__ float sm_l[W][16];
-  __shared__ __attribute__((aligned(16))) float sm_acc[W][16][D + 4];
+  // the waves' states of a fold round: [wave][column tile][d-tile][lane]
+  // (acc) and [wave][column tile][lane] (m, l)
+  constexpr int kFold = W * fold_tiles<D>();
+  __shared__ f32x4 sm_facc[kFold * Geo<D>::NT * kWave];
+  __shared__ float2 sm_fml[kFold * kWave];
   __shared__ f16x8 sm_q[CIE_MIXED_QLDS ? col_group<D>() * Geo<D>::KS * kWave : 1];
   __shared__ int sm_last;
-  __shared__ int sm_prefix[kMaxSeqs + 1];
   __shared__ int sm_scan[NTH];
-  // the plan's view of each sequence (seq_info), so an item starts its Q and
-  // page-id loads without reading the sequence tables again
-  __shared__ int64_t sm_t0[kMaxSeqs];
-  __shared__ int sm_slot[kMaxSeqs], sm_rows[kMaxSeqs], sm_prior[kMaxSeqs];
+  // The plan, in LDS sized by the launch to the batch (mixed_plan_lds): the
+  // item prefix per sequence and each sequence's seq_info, so an item starts
+  // its Q and page-id loads without reading the sequence tables again.
+  extern __shared__ __attribute__((aligned(16))) char sm_plan[];
+  int64_t* const sm_t0 = reinterpret_cast<int64_t*>(sm_plan);
+  int* const sm_slot = reinterpret_cast<int*>(sm_t0 + p.B);
+  int* const sm_rows = sm_slot + p.B;
+  int* const sm_prior = sm_rows + p.B;
+  int* const sm_prefix = sm_prior + p.B;  // B + 1 entries
 
   constexpr int CG = col_group<D>();
   const int g = blockIdx.y;
@@ -581,7 +643,7 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     }
     MIXED_TRACE(item, 1, __builtin_amdgcn_s_memrealtime());
     MIXED_TRACE(item, 7, (uint64_t)(b * 1000 + qt));
-    process_item<D>(p, s, b, g, uniform(qt), uniform(j), sm_m, sm_l, sm_acc, sm_q, &sm_last, item);
+    process_item<D>(p, s, b, g, uniform(qt), uniform(j), sm_facc, sm_fml, sm_q, &sm_last, item);
   }
 }
 
@@ -597,7 +659,8 @@ static int mixed_workgroups(int H_kv) {
 template <int D>
 static int launch_mixed(const MixedParams& p, hipStream_t stream) {
   dim3 grid(mixed_workgroups(p.H_kv), p.H_kv, 1);
-  hipLaunchKernelGGL((mixed_attention_kernel<D>), grid, dim3(mixed_waves<D>() * kWave), 0, stream, p);
+  hipLaunchKernelGGL((mixed_attention_kernel<D>), grid, dim3(mixed_waves<D>() * kWave),
+                     mixed_plan_lds(p.B), stream, p);
   return (int)hipGetLastError();
 }
 
