@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from custom_inference_engine_amd import _native, decode_gqa_attention
+from custom_inference_engine_amd import _native, decode_gqa_attention, mixed_gqa_attention
 from oracle import inputs
 from tests.conftest import assert_attn_close
 from tests.golden.make_golden import INPUT_FIELDS, build_case, digest
@@ -70,6 +70,29 @@ def test_mixed_long_prefixes_split_keys(native_lib, prior, new, d):
     note(f"mixed long prefixes prior={prior} new={new} D={d}")
     kp, vp, o = gpu_mixed_step(case)
     _check(case, o, f"long {prior}/{new} D={d}")
+
+
+def test_mixed_largest_batch(native_lib):
+    """1,024 sequences, the kernel's limit: its plan tables (24 B per sequence)
+    take LDS sized to the batch, here the largest allocation it makes."""
+    g = torch.Generator().manual_seed(39)
+    prior = torch.randint(0, 48, (1024,), generator=g).tolist()
+    new = torch.randint(0, 3, (1024,), generator=g).tolist()
+    case = inputs.make_case(prior, new, seed=39)
+    note("mixed 1024 sequences")
+    kp, vp, o = gpu_mixed_step(case)
+    ko, vo = case.appended_pools()
+    assert torch.equal(bits(kp), bits(ko)) and torch.equal(bits(vp), bits(vo))
+    _check(case, o, "1024 sequences")
+
+
+def test_mixed_batch_above_the_plan_limit_is_rejected(native_lib):
+    case = inputs.make_case([2] * 1025, seed=40)
+    note("mixed 1025 sequences (rejected)")
+    c = case.to(DEV)
+    with pytest.raises(RuntimeError, match="unsupported shape"):
+        mixed_gqa_attention(c.q, c.k_pool, c.v_pool, 1, c.cu_seqlens, c.kv_lens, c.slot_ids,
+                            c.block_table)
 
 
 def test_mixed_partials_above_2gib_in_the_low_address_word(native_lib):
