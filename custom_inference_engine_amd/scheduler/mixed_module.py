@@ -14,10 +14,16 @@ decoder stack of one token bucket in a hipGraph, like the reference's
 a fixed number of sequences with the reserved slot and zero-length chunks
 (``cu_seqlens`` padded with its last value), pages / offsets with page 0, and
 ``max_seqlen`` is the token bucket; the varlen kernel plans its work on the
-device, so padded sequences cost nothing.  The reference runs its larger
-buckets through a piecewise ``torch.compile`` backend instead; here every
-bucket can be a full graph, because one graph per token bucket (at the
-largest batch) covers every batch size.
+device, so padded sequences cost nothing.
+
+``PiecewiseMixedModule`` is the reference's module for its larger token
+buckets (scheduler/mixed_module.py:216-249): ``torch.compile`` of the stack
+(``fullgraph=True``, ``dynamic=False``, the batch dimension of ``slot_ids`` and
+``cu_seqlens`` marked dynamic) through the piecewise backend, which replays the
+code between attention calls from hipGraphs and runs the varlen attention
+eagerly into a shared buffer; the batch is not padded.  Here one full graph
+per token bucket already covers every batch size, so the scheduler uses the
+piecewise module only when asked to.
 """
 from __future__ import annotations
 
@@ -25,6 +31,7 @@ import torch
 import torch.nn.functional as F
 
 from ..attn.metadata import AttentionMetadata
+from ..piecewise import get_piecewise_backend
 from .slots import pad_slot_ids
 
 
@@ -58,6 +65,13 @@ class MixedModule:
 
     def replay(self) -> torch.Tensor:
         return self._forward()
+
+    def warmup(self, n: int) -> None:
+        """One real step through slots 1..n (then reset), as the reference's warm-up does
+        (scheduler/mixed_module.py:41-47)."""
+        slot_ids = list(range(1, n + 1))
+        self.forward([[0] * (self.token_count // n) for _ in slot_ids], slot_ids)
+        self.kv_cache.reset(slot_ids)
 
     # -- the step
 
@@ -130,12 +144,6 @@ class FullMixedModule(MixedModule):
         self.lens = self.static_lens
         self.warmup(min(batch_size, kv_cache.n_slots - 1, token_count))
 
-    def warmup(self, n: int) -> None:
-        """One real step through slots 1..n (then reset), as the reference's warm-up does."""
-        slot_ids = list(range(1, n + 1))
-        self.forward([[0] * (self.token_count // n) for _ in slot_ids], slot_ids)
-        self.kv_cache.reset(slot_ids)
-
     def _pad(self, slot_ids: list[int]) -> list[int]:
         return pad_slot_ids(slot_ids, self.batch_size, self.kv_cache.unused_idx)
 
@@ -147,3 +155,28 @@ class FullMixedModule(MixedModule):
     def replay(self) -> torch.Tensor:
         self.graph.replay()
         return self.static_hidden
+
+
+class PiecewiseMixedModule(MixedModule):
+    """The stack compiled through the piecewise backend (see the module docstring).
+
+    ``buffer`` (1, >= token_count, H_q, D) receives the attention outputs; it can
+    be shared by the modules of every token bucket, as in the reference.
+    """
+
+    def __init__(self, model, kv_cache, token_count: int, buffer: torch.Tensor, pool=None):
+        super().__init__(model, kv_cache, token_count)
+        self.compiled = torch.compile(self._forward,
+                                      backend=get_piecewise_backend(buffer[:, :token_count], pool),
+                                      fullgraph=True, dynamic=False)
+        self.warmup(min(kv_cache.n_slots - 1, token_count))
+        self.warmup(1)
+
+    def _write_batch(self, slots: torch.Tensor, cu_seqlens: torch.Tensor, lens: torch.Tensor) -> None:
+        if len(slots) > 1:
+            torch._dynamo.mark_dynamic(slots, 0)
+            torch._dynamo.mark_dynamic(cu_seqlens, 0)
+        super()._write_batch(slots, cu_seqlens, lens)
+
+    def replay(self) -> torch.Tensor:
+        return self.compiled()

@@ -125,15 +125,18 @@ class ModuleExecutor:
     ``DecodeModule`` per batch bucket and, with ``graph_mixed``, one
     ``FullMixedModule`` per token bucket at the largest batch bucket.
     Without it, mixed steps run eagerly (``MixedModule`` of the token bucket,
-    made on first use).
+    made on first use).  With ``piecewise_above`` set, the token buckets above
+    it use ``PiecewiseMixedModule`` instead, sharing one attention-output
+    buffer, as the reference's ``PiecewiseGraphBackend`` does for buckets above
+    its full-graph threshold (scheduler/graph_backend.py:64-95).
     """
 
     def __init__(self, model, kv_cache, batch_sizes: list[int], token_counts: list[int], pool=None,
-                 graph_mixed: bool = True):
+                 graph_mixed: bool = True, piecewise_above: int | None = None):
         import torch
 
         from .decode_module import DecodeModule
-        from .mixed_module import FullMixedModule
+        from .mixed_module import FullMixedModule, PiecewiseMixedModule
 
         self.model = model
         self.kv_cache = kv_cache
@@ -143,10 +146,21 @@ class ModuleExecutor:
                                for b in sorted(batch_sizes, reverse=True)}
         self.max_batch = max(batch_sizes)
         self.mixed_modules = {}
+        piecewise = [t for t in self.token_counts if piecewise_above is not None and t > piecewise_above]
+        if graph_mixed and piecewise:
+            # two compiles per bucket (batch 1 and a dynamic batch), on one code object
+            torch._dynamo.config.recompile_limit = max(torch._dynamo.config.recompile_limit,
+                                                       2 * len(piecewise))
+            self.buffer = torch.zeros((1, max(piecewise), kv_cache.num_q_heads, kv_cache.head_dim),
+                                      dtype=kv_cache.dtype, device=kv_cache.device)
         if graph_mixed:
             for t in sorted(self.token_counts, reverse=True):
-                self.mixed_modules[t] = FullMixedModule(model, kv_cache, batch_size=self.max_batch,
-                                                        token_count=t, pool=self.pool)
+                if t in piecewise:
+                    self.mixed_modules[t] = PiecewiseMixedModule(model, kv_cache, token_count=t,
+                                                                 buffer=self.buffer, pool=self.pool)
+                else:
+                    self.mixed_modules[t] = FullMixedModule(model, kv_cache, batch_size=self.max_batch,
+                                                            token_count=t, pool=self.pool)
 
     def decode_module(self, n: int):
         return self.decode_modules[_smallest_fit(self.decode_modules, n)]
@@ -185,7 +199,8 @@ class Scheduler:
     SENTINEL: ClassVar[object] = object()
 
     def __init__(self, model, kv_cache, eos_token_ids: set[int], max_new_tokens: int,
-                 token_budget: int, executor: StepExecutor | None = None) -> None:
+                 token_budget: int, executor: StepExecutor | None = None,
+                 piecewise_mixed: bool = False) -> None:
         n_slots = kv_cache.n_slots
         if n_slots <= 1:
             raise ValueError("n_slots must be greater than 1.")
@@ -216,7 +231,8 @@ class Scheduler:
         self.token_counts = token_buckets(token_budget, self.MIN_TOKEN_BUCKET,
                                           self.FULL_GRAPH_TOKEN_THRESHOLD, self.PIECEWISE_TOKEN_STEP)
         self.executor = executor if executor is not None else ModuleExecutor(
-            model, kv_cache, self.batch_sizes, self.token_counts)
+            model, kv_cache, self.batch_sizes, self.token_counts,
+            piecewise_above=self.FULL_GRAPH_TOKEN_THRESHOLD if piecewise_mixed else None)
 
         self.stats = RunStats()
         self.requests: queue.Queue = queue.Queue()

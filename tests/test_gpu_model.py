@@ -107,3 +107,51 @@ def test_full_mixed_module_graph_matches_eager(native_lib):
     assert torch.equal(lens_a, lens_b) and lens_a[slots].tolist() == [len(p) + 1 for p in prompts]
     assert torch.allclose(la, lb, rtol=1e-3, atol=1e-3)
     assert torch.allclose(k_a[1:].float(), k_b[1:].float(), rtol=1e-3, atol=1e-3)  # page 0: padding
+
+
+def test_piecewise_mixed_module_matches_eager(native_lib):
+    """Steps through PiecewiseMixedModule (hipGraph pieces between eager varlen
+    attention calls, batch dimension dynamic) equal the eager module's: a prefill
+    of three prompts, decode rows for them, then batches of one and two sequences
+    (the batch-1 compile, then the dynamic one again)."""
+    from custom_inference_engine_amd.scheduler import PiecewiseMixedModule
+
+    cfg, ref = _model()
+    ours = copy.deepcopy(ref).half().to(DEV)
+    use_triton_attention(ours)
+    g = torch.Generator().manual_seed(21)
+    prompts = [torch.randint(0, 512, (n,), generator=g).tolist() for n in (37, 5, 20)]
+    slots = [1, 2, 3]
+    results = []
+    for piecewise in (False, True):
+        torch._dynamo.reset()
+        kv = KVStorage(cfg, max_cache_len=2048, page_size=16, n_slots=5, device=DEV, dtype=torch.float16)
+        note(f"mixed module, piecewise={piecewise}")
+        if piecewise:
+            buffer = torch.zeros((1, 64, kv.num_q_heads, kv.head_dim), dtype=torch.float16, device=DEV)
+            mod = PiecewiseMixedModule(ours, kv, token_count=64, buffer=buffer,
+                                       pool=torch.cuda.graph_pool_handle())
+        else:
+            mod = MixedModule(ours, kv, token_count=64)
+        free = (torch.randperm(kv.n_pages - 1, generator=torch.Generator().manual_seed(3)) + 1).tolist()
+        for s, p in zip(slots, prompts):
+            assign_pages(kv, s, len(p) + 8, free)
+        steps = [mod.forward(prompts, slots)]
+        logits = [mod.last_logits.float().cpu()]
+        steps.append(mod.forward([[t] for t in steps[-1]], slots))
+        logits.append(mod.last_logits.float().cpu())
+        steps.append(mod.forward([[steps[-1][1], 7, 9]], [2]))
+        logits.append(mod.last_logits.float().cpu())
+        steps.append(mod.forward([[steps[-2][0]], [steps[-2][2], 3]], [1, 3]))
+        logits.append(mod.last_logits.float().cpu())
+        torch.cuda.synchronize()
+        results.append((steps, logits, kv.lens.cpu(), torch.stack(kv.keys).cpu(), torch.stack(kv.values).cpu()))
+    (sa, la, lens_a, k_a, v_a), (sb, lb, lens_b, k_b, v_b) = results
+    assert sa == sb
+    assert torch.equal(lens_a, lens_b)
+    assert lens_a[slots].tolist() == [len(p) + d for p, d in zip(prompts, (2, 4, 3))]
+    for x, y in zip(la, lb):
+        assert torch.allclose(x, y, rtol=1e-3, atol=1e-3)
+    # page 0 holds the padding tokens' appends
+    assert torch.allclose(k_a[:, 1:].float(), k_b[:, 1:].float(), rtol=1e-3, atol=1e-3)
+    assert torch.allclose(v_a[:, 1:].float(), v_b[:, 1:].float(), rtol=1e-3, atol=1e-3)

@@ -21,7 +21,11 @@ from tests.gpu_helpers import DEV, note
 pytestmark = pytest.mark.gpu
 
 
-def test_scheduler_serves_prompts_with_preemption(native_lib):
+@pytest.mark.parametrize("piecewise", [False, True], ids=["full_graphs", "piecewise_above_128"])
+def test_scheduler_serves_prompts_with_preemption(native_lib, piecewise):
+    """``piecewise``: token buckets above 128 run through ``PiecewiseMixedModule``,
+    as in the reference's scheduler (scheduler/scheduler.py:157-200)."""
+    torch._dynamo.reset()
     cfg = Qwen2Config(hidden_size=896, num_attention_heads=14, num_key_value_heads=2,
                       intermediate_size=1024, num_hidden_layers=2, vocab_size=512,
                       max_position_embeddings=4096, rope_theta=1e6, rms_norm_eps=1e-6,
@@ -33,7 +37,8 @@ def test_scheduler_serves_prompts_with_preemption(native_lib):
     use_triton_attention(ours)
     kv = KVStorage(cfg, max_cache_len=192, page_size=16, n_slots=4, device=DEV, dtype=torch.float16)
     note("scheduler: capturing decode buckets")
-    sched = Scheduler(ours, kv, eos_token_ids={cfg.vocab_size}, max_new_tokens=16, token_budget=160)
+    sched = Scheduler(ours, kv, eos_token_ids={cfg.vocab_size}, max_new_tokens=16, token_budget=160,
+                      piecewise_mixed=piecewise)
 
     g = torch.Generator().manual_seed(11)
     prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in (60, 70, 50, 9, 64)]
@@ -43,6 +48,7 @@ def test_scheduler_serves_prompts_with_preemption(native_lib):
     torch.cuda.synchronize()
     assert sched.stats.preemptions == 2
     assert sched.stats.mixed_steps and sched.stats.decode_steps
+    assert sched.stats.mixed_steps[160] > 0  # the bucket above 128 ran
 
     for i, (p, r) in enumerate(zip(prompts, results)):
         assert len(r.new_tokens) == 16
