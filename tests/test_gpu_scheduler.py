@@ -15,7 +15,7 @@ import torch
 from transformers import Qwen2Config, Qwen2ForCausalLM
 
 from custom_inference_engine_amd import KVStorage, use_triton_attention
-from custom_inference_engine_amd.scheduler import Scheduler
+from custom_inference_engine_amd.scheduler import FullMixedModule, PiecewiseMixedModule, Scheduler
 from tests.gpu_helpers import DEV, note
 
 pytestmark = pytest.mark.gpu
@@ -49,6 +49,8 @@ def test_scheduler_serves_prompts_with_preemption(native_lib, piecewise):
     assert sched.stats.preemptions == 2
     assert sched.stats.mixed_steps and sched.stats.decode_steps
     assert sched.stats.mixed_steps[160] > 0  # the bucket above 128 ran
+    kind = PiecewiseMixedModule if piecewise else FullMixedModule
+    assert type(sched.executor.mixed_module(160)) is kind
 
     for i, (p, r) in enumerate(zip(prompts, results)):
         assert len(r.new_tokens) == 16
