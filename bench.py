@@ -154,6 +154,28 @@ def cpu_baseline(case, budget_s: float = 20.0, max_runs: int = 7):
     return statistics.median(runs) * 1e6, len(runs), torch.get_num_threads(), out
 
 
+_bench_lib = None
+
+
+def bench_lib():
+    """libcie_bench.so: bench-only measurement kernels, kept out of the product
+    library (built by the package's build_bench(), here if it is missing)."""
+    global _bench_lib
+    if _bench_lib is None:
+        import ctypes
+
+        from custom_inference_engine_amd import _build
+
+        if not os.path.exists(_build.BENCH_LIB_PATH):
+            _build.build_bench()
+        lib = ctypes.CDLL(_build.BENCH_LIB_PATH)
+        p, i64 = ctypes.c_void_p, ctypes.c_int64
+        lib.cie_bench_gather_read.restype = ctypes.c_int
+        lib.cie_bench_gather_read.argtypes = [p, p, i64, i64, i64, p, p]
+        _bench_lib = lib
+    return _bench_lib
+
+
 def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chunk: int = 2048,
                    region_bytes: int = 1 << 30):
     """HBM ceiling of the paged access pattern on this box: the probe kernel reads
@@ -161,7 +183,7 @@ def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chun
     1 GiB region (R disjoint chunk lists rotate, so the 256 MB MALL cannot help)."""
     from custom_inference_engine_amd import _native
 
-    lib = _native.load()
+    lib = bench_lib()
     region = torch.ones(region_bytes, dtype=torch.uint8, device=dev)
     n_region = region.numel() // chunk
     n = nbytes // chunk
@@ -172,9 +194,10 @@ def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chun
 
     def f(i):
         def g():
-            _native.check(lib.cie_probe_gather_read(region.data_ptr(), lists[i].data_ptr(), n, chunk, 2048,
-                                                    sink.data_ptr(), _native.stream_handle(dev)),
-                          "cie_probe_gather_read")
+            rc = lib.cie_bench_gather_read(region.data_ptr(), lists[i].data_ptr(), n, chunk, 2048,
+                                           sink.data_ptr(), _native.stream_handle(dev))
+            if rc != 0:
+                raise RuntimeError(f"cie_bench_gather_read failed: status {rc}")
         return g
 
     us, _ = time_calls([f(i) for i in range(R)], steps, warmup, True, repeats)

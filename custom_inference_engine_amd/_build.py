@@ -4,6 +4,9 @@ The library is compiled straight from ``csrc/*.hip`` for gfx950 only; the built
 ``.so`` sits next to this file so it travels with the source tree.  Objects go
 to ``_build/`` and the final link replaces the library atomically.
 
+bench.py's measurement helpers (``csrc/bench/``) build into a separate
+``libcie_bench.so`` (``build_bench``); the product library never contains them.
+
 Tuning variants (the kernels' ``CIE_*`` build-time settings) build elsewhere:
 ``python -m custom_inference_engine_amd._build -D CIE_MIXED_NARROW_PAIRS=6 --out DIR``
 writes ``DIR/libcie_paged.so``, which the loader takes from ``CIE_PAGED_LIB``.
@@ -23,7 +26,10 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libcie_paged.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ("capi.hip", "kv_append.hip", "paged_decode.hip", "mixed_attention.hip", "probe.hip")
+SOURCES = ("capi.hip", "kv_append.hip", "paged_decode.hip", "mixed_attention.hip")
+# bench.py's measurement helpers: a library of their own, never linked into the product
+BENCH_SOURCES = ("bench/gather_probe.hip",)
+BENCH_LIB_PATH = os.path.join(PKG_DIR, "libcie_bench.so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in device code.
@@ -50,7 +56,7 @@ def hipcc() -> str:
 
 
 def _compile(src: str, verbose: bool, obj_dir: str = BUILD_DIR, defines: tuple = ()) -> str:
-    obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
+    obj = os.path.join(obj_dir, os.path.splitext(src)[0].replace("/", "_") + ".o")
     cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), "-I", INCLUDE, "-I", CSRC, "-c",
            os.path.join(CSRC, src), "-o", obj, "-Rpass-analysis=kernel-resource-usage"]
     if verbose:
@@ -72,6 +78,18 @@ def _compile(src: str, verbose: bool, obj_dir: str = BUILD_DIR, defines: tuple =
     return obj
 
 
+def _link(objs: list, lib_path: str, verbose: bool) -> str:
+    tmp = lib_path + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, lib_path)
+    return lib_path
+
+
 def build(verbose: bool = False, defines: tuple = (), out_dir: str | None = None) -> str:
     """Compile every HIP source for gfx950 and link ``libcie_paged.so`` (in-tree, or a
     tuning variant with extra ``NAME=VALUE`` defines into ``out_dir``)."""
@@ -82,15 +100,14 @@ def build(verbose: bool = False, defines: tuple = (), out_dir: str | None = None
     os.makedirs(obj_dir, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose, obj_dir, tuple(defines)), SOURCES))
-    tmp = lib_path + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
-    os.replace(tmp, lib_path)
-    return lib_path
+    return _link(objs, lib_path, verbose)
+
+
+def build_bench(verbose: bool = False) -> str:
+    """Compile bench.py's measurement helpers into ``libcie_bench.so`` (in-tree)."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    objs = [_compile(s, verbose, BUILD_DIR) for s in BENCH_SOURCES]
+    return _link(objs, BENCH_LIB_PATH, verbose)
 
 
 if __name__ == "__main__":
@@ -103,3 +120,5 @@ if __name__ == "__main__":
     ap.add_argument("--out", default=None, help="directory of a variant build")
     a = ap.parse_args()
     print(build(verbose=a.v, defines=tuple(a.defines), out_dir=a.out))
+    if not a.out:
+        print(build_bench(verbose=a.v))

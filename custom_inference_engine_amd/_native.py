@@ -73,12 +73,9 @@ _SIGNATURES = {
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
-    "cie_probe_gather_read": (
-        ctypes.c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
-    ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -35,10 +35,8 @@ from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention, apply_rotar
 
 from .. import _native
 
-# Decode kernel geometry: one split = one workgroup of 8 wavefronts, which is
-# what one CU holds at the kernel's register use; the split count aims at one
-# workgroup per CU (MI355X: 256 CUs), i.e. one resident round.
-DECODE_WAVES_PER_SPLIT = 8
+# Decode kernel geometry: one split = one workgroup; the split count aims at
+# one workgroup per CU (MI355X: 256 CUs), i.e. one resident round.
 DECODE_DEFAULT_CUS = 256
 DECODE_MAX_SPLITS = 64
 
@@ -68,11 +66,13 @@ _ctr_retired: list[torch.Tensor] = []
 def split_counters(dev: torch.device, n: int) -> torch.Tensor:
     """The device's persistent split-arrival counters (zeroed once, kept zero by the kernels).
 
-    The decode and mixed kernels' counters must be zero before a call and are
-    left zero by it, so one buffer serves every stream-ordered call on a
-    device, graph replays included, without a clearing launch.  Calls that can
-    overlap in time (different streams) must pass their own zeroed ``counters``.
-    Replaced buffers stay alive: a captured graph may still point at them.
+    The decode and mixed kernels' counters (arrival words, then as many stale
+    words) must be zero before a call and are left zero by it, so one buffer
+    serves every stream-ordered call on a device, graph replays included,
+    without a clearing launch.  Calls that can overlap in time (different
+    streams) must pass their own zeroed ``counters``; a kernel that finds a
+    stale word raises ``CIE_ERRBIT_SPLIT`` in ``err``.  Replaced buffers stay
+    alive: a captured graph may still point at them.
     """
     with _ctr_lock:
         buf = _ctr_cache.get(dev.index)
@@ -88,8 +88,8 @@ def _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters):
     partials = torch.empty(lib.cie_paged_decode_partials_bytes(B, H_q, D, P), dtype=torch.uint8,
                            device=dev)
     if counters is None:
-        counters = split_counters(dev, B * H_kv)
-    _require(counters.dtype == torch.int32 and counters.numel() >= B * H_kv, "counters too small")
+        counters = split_counters(dev, 2 * B * H_kv)
+    _require(counters.dtype == torch.int32 and counters.numel() >= 2 * B * H_kv, "counters too small")
     return partials, counters
 
 

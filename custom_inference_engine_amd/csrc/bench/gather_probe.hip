@@ -1,15 +1,21 @@
-// Measurement helper: the HBM read ceiling for a paged access pattern.
+// Bench-only measurement helper (built into libcie_bench.so, never into the
+// product library): the HBM read ceiling of a paged access pattern.
 //
-// Reads n_chunks chunks of chunk_bytes each (chunk i at base + ids[i] *
-// chunk_bytes), 16 bytes per lane per non-temporal load (the decode's KV
-// load policy, and the fastest one measured for this pattern), four chunks
-// in flight per wavefront, and folds the data into one word so the loads
-// cannot be removed.  With the chunk size of a KV page-head (2 KiB) and shuffled ids it
-// is the paged decode's memory traffic without any of its math, i.e. the
-// attainable bandwidth the decode kernel is judged against.
-#include "cie_common.h"
+// cie_bench_gather_read reads n_chunks chunks of chunk_bytes each (chunk i at
+// base + ids[i] * chunk_bytes), 16 bytes per lane per non-temporal load (the
+// decode's V-row load policy, the fastest one measured for this pattern),
+// four chunks in flight per wavefront, and folds the data into one word so
+// the loads cannot be removed.  With the chunk size of a KV page-head
+// (2 KiB) and shuffled ids it is the paged decode's memory traffic without
+// any of its math: the attainable bandwidth the decode kernel is judged
+// against.  No counterpart in the reference.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
 
-namespace cie {
+namespace cie_bench {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kWave = 64;
 
 template <int CHUNK16>  // 16-byte words per chunk (a multiple of 64)
 __global__ __launch_bounds__(256) void gather_read_kernel(const u32x4* __restrict__ base,
@@ -27,7 +33,7 @@ __global__ __launch_bounds__(256) void gather_read_kernel(const u32x4* __restric
       const int64_t id = (c + j < n_chunks) ? ids[c + j] : ids[c];
       const u32x4* p = base + id * CHUNK16;
 #pragma unroll
-      for (int k = 0; k < PER_LANE; ++k) v[j][k] = stream_load(p + k * kWave + lane);
+      for (int k = 0; k < PER_LANE; ++k) v[j][k] = __builtin_nontemporal_load(p + k * kWave + lane);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -37,18 +43,20 @@ __global__ __launch_bounds__(256) void gather_read_kernel(const u32x4* __restric
   if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u) sink[0] = 1u;
 }
 
-}  // namespace cie
+}  // namespace cie_bench
 
-using namespace cie;
+using namespace cie_bench;
 
-extern "C" int cie_probe_gather_read(const void* base, const int32_t* chunk_ids, int64_t n_chunks,
+// 0 on success, -1 for bad arguments, -2 for an unsupported chunk size, else
+// the hipError_t of the launch.
+extern "C" int cie_bench_gather_read(const void* base, const int32_t* chunk_ids, int64_t n_chunks,
                                      int64_t chunk_bytes, int64_t n_workgroups, uint32_t* sink,
                                      void* stream) {
   if (!base || !chunk_ids || !sink || n_chunks < 0 || n_workgroups <= 0 ||
       n_workgroups > 0x7fffffff)
-    return CIE_EINVAL;
-  if (reinterpret_cast<uintptr_t>(base) & 15) return CIE_EINVAL;
-  if (n_chunks == 0) return CIE_OK;
+    return -1;
+  if (reinterpret_cast<uintptr_t>(base) & 15) return -1;
+  if (n_chunks == 0) return 0;
   const dim3 grid((unsigned)n_workgroups);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const u32x4* b = static_cast<const u32x4*>(base);
@@ -56,7 +64,7 @@ extern "C" int cie_probe_gather_read(const void* base, const int32_t* chunk_ids,
     case 1024: hipLaunchKernelGGL(gather_read_kernel<64>, grid, dim3(256), 0, s, b, chunk_ids, n_chunks, sink); break;
     case 2048: hipLaunchKernelGGL(gather_read_kernel<128>, grid, dim3(256), 0, s, b, chunk_ids, n_chunks, sink); break;
     case 4096: hipLaunchKernelGGL(gather_read_kernel<256>, grid, dim3(256), 0, s, b, chunk_ids, n_chunks, sink); break;
-    default: return CIE_EUNSUPPORTED;
+    default: return -2;
   }
   return (int)hipGetLastError();
 }

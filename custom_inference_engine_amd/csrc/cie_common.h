@@ -97,9 +97,7 @@ __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
 }
 
 __device__ __forceinline__ void set_err(int32_t* err, int bit) {
-#ifndef CIE_DECODE_TRACE
   if (err) atomicOr(err, bit);
-#endif
 }
 
 // Device-coherent (agent-scope) accesses: global_store / global_load with sc1,
@@ -131,17 +129,58 @@ __device__ __forceinline__ void agent_store4(__amdgpu_buffer_rsrc_t r, uint32_t 
 __device__ __forceinline__ f32x4 agent_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kBufSc1));
 }
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+// s_waitcnt vmcnt(0): every vector-memory access this wave issued has
+// completed (stores included: on gfx9 they count in vmcnt).  The intrinsic
+// touches no memory as far as LLVM is concerned, so compiler-only fences on
+// both sides pin the agent-scope stores before it and the arrival atomic
+// after it; tests/test_asm_order.py checks the order in the built code.
+__device__ __forceinline__ void wait_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
-// Last-arriver election: every workgroup of a group calls this once after its
-// partial results are stored with agent_store; exactly one (the last) gets
-// true.  Resetting the counter to zero is up to the winner.
-__device__ __forceinline__ bool arrive_last(int32_t* counter, int n_members, int* sm_flag) {
+// Split arrival counters.  A group of n_members workgroups that each store a
+// partial result (with agent_store / agent_store4) elects its last arriver
+// with one relaxed agent-scope fetch_add on the group's arrival word; the
+// winner merges and puts the word back to zero, so a buffer of zeros stays
+// zeros across stream-ordered calls.  Ordering (gfx950, LLVM AMDGPU memory
+// model, GFX942 family): relaxed agent-scope stores, loads and RMWs are
+// global_store / global_load / global_atomic with sc1, each coherent at agent
+// scope by itself; the partial stores have completed (vmcnt(0)) before the
+// atomic is issued, and the winner's sc1 loads are issued after the atomic
+// returned, so they read the completed stores.  No L2 writeback
+// (buffer_wbl2) or invalidate is needed, because no partial is ever accessed
+// without sc1.
+//
+// A word outside [0, n_members) at the start of a call (a caller's unzeroed
+// buffer, a call that overlapped another on the same counters) is detected:
+// an arrival that reads such a value raises CIE_ERRBIT_SPLIT and counts
+// itself on the group's stale word, n_words further on.  When every arrival
+// of a call reads a stale value (the word held n_members or more, or was
+// negative enough), the last of them puts both words back to zero, so the
+// next call is clean; a stale value below n_members is not distinguishable
+// from live arrivals and is reported only by the arrivals that overshoot.
+__device__ __forceinline__ void counter_reset(int32_t* word) {
+  __hip_atomic_store(word, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool arrive_last(int32_t* arrival, int64_t n_words, int n_members,
+                                            int* sm_flag, int32_t* err) {
   wait_stores();
   __syncthreads();
-  if (threadIdx.x == 0)
-    *sm_flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               n_members - 1;
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(arrival, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *sm_flag = old == n_members - 1;
+    if (old < 0 || old >= n_members) {
+      if (err) atomicOr(err, CIE_ERRBIT_SPLIT);
+      int32_t* stale = arrival + n_words;
+      if (__hip_atomic_fetch_add(stale, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          n_members - 1) {
+        counter_reset(arrival);
+        counter_reset(stale);
+      }
+    }
+  }
   __syncthreads();
   return *sm_flag != 0;
 }

@@ -107,7 +107,7 @@ struct MixedParams {
   float* part_m;  // [total_T][H_q][kMaxChunks]
   float* part_l;
   float* part_acc;  // [total_T][H_q][kMaxChunks][D]
-  int32_t* counters;  // [B][H_kv][n_qtiles][kMaxColGroups], zero between calls
+  int32_t* counters;  // 2 x [B][H_kv][n_qtiles][kMaxColGroups]: arrival words, then stale words
   int64_t pool_page_stride, pool_head_stride, bt_stride, n_pages, total_T;
   int32_t bt_width, n_slots, B, H_q, H_kv, G, page_size, n_qtiles;
   float scale_log2;
@@ -216,15 +216,17 @@ __device__ __forceinline__ int column_off(const MixedParams& p, int g, int cc) {
 }
 
 // Profiling builds only (-DCIE_MIXED_TRACE): thread 0 stamps each work item's
-// phases (s_memrealtime) into the buffer passed as `err`, 16 words per
+// phases (s_memrealtime) into a trace buffer of its own, named by
+// cie_mixed_trace_buffer() (exported by such builds alone), 16 words per
 // (kv head, item).
 #ifdef CIE_MIXED_TRACE
-#define MIXED_TRACE(item, k, v)                                                                  \
-  do {                                                                                           \
-    if (threadIdx.x == 0 && p.err != nullptr && (item) < 4096) {                                 \
-      __builtin_amdgcn_s_waitcnt(0);                                                             \
-      reinterpret_cast<uint64_t*>(p.err)[((int64_t)blockIdx.y * 4096 + (item)) * 16 + (k)] = (v); \
-    }                                                                                            \
+__device__ uint64_t* g_mixed_trace;
+#define MIXED_TRACE(item, k, v)                                                     \
+  do {                                                                              \
+    if (threadIdx.x == 0 && g_mixed_trace != nullptr && (item) < 4096) {            \
+      __builtin_amdgcn_s_waitcnt(0);                                                \
+      g_mixed_trace[((int64_t)blockIdx.y * 4096 + (item)) * 16 + (k)] = (v);        \
+    }                                                                               \
   } while (0)
 #else
 #define MIXED_TRACE(item, k, v) \
@@ -523,10 +525,11 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   // The last chunk of this (tile, column group) to arrive merges all chunks.
   int32_t* ctr =
       p.counters + (((int64_t)b * p.H_kv + g) * p.n_qtiles + qt) * kMaxColGroups + gi;
-  if (arrive_last(ctr, tp.n_chunks, sm_last)) {
+  const int64_t n_words = (int64_t)p.B * p.H_kv * p.n_qtiles * kMaxColGroups;
+  if (arrive_last(ctr, n_words, tp.n_chunks, sm_last, p.err)) {
     MIXED_TRACE(item, 4, __builtin_amdgcn_s_memrealtime());
     merge_group<D>(p, s, tp, g, ct0, min(16 * n, tp.n_combos - 16 * ct0));
-    if (threadIdx.x == 0) *ctr = 0;
+    if (threadIdx.x == 0) counter_reset(ctr);
   }
   __syncthreads();
   MIXED_TRACE(item, 3, __builtin_amdgcn_s_memrealtime());
@@ -691,8 +694,18 @@ extern "C" int64_t cie_mixed_partials_bytes(int64_t total_T, int64_t H_q, int64_
 
 extern "C" int64_t cie_mixed_counters(int64_t B, int64_t H_kv, int64_t max_seqlen) {
   if (B < 0 || H_kv <= 0 || max_seqlen < 0) return -1;
-  return B * H_kv * ((max_seqlen + 15) / 16) * kMaxColGroups;
+  // arrival words, then as many stale words (arrive_last)
+  return 2 * B * H_kv * ((max_seqlen + 15) / 16) * kMaxColGroups;
 }
+
+#ifdef CIE_MIXED_TRACE
+// Trace builds only: where the mixed kernel stamps its phases (device buffer
+// of 16 uint64 per (kv head, item); NULL turns the stamps off).
+extern "C" int cie_mixed_trace_buffer(void* buf) {
+  uint64_t* p = static_cast<uint64_t*>(buf);
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_mixed_trace), &p, sizeof(p));
+}
+#endif
 
 extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, const void* v_pool,
                                    const int64_t* cu_seqlens, const int64_t* kv_lens,

@@ -20,32 +20,27 @@
 //    the pool receives the rotated K row.
 //
 // Work split.  Grid (n_splits, H_kv, B), WAVES wavefronts per workgroup.  The
-// reference interleaves 16-row blocks over its P programs
-// (kernels/decode_attention.py:71-75); here the ceil(L/16) key tiles of a
-// (sequence, kv head) are cut into n_splits * WAVES contiguous, balanced runs,
-// one per wave.  A wave keeps the G query heads of its kv head as MFMA columns
-// (attn_engine.h); the waves of a workgroup fold their softmax states through
-// LDS.  With one split the workgroup writes o directly.  Otherwise it writes a
-// partial (m, l, acc) per head, and the last workgroup of the (sequence, kv
-// head) to finish — found with a device-scope counter — merges the splits with
-// log-sum-exp as kernels/decode_attention.py:243-264 does, writes o and resets
-// the counter to zero for the next call.
+// ceil(L/16) key tiles of a (sequence, kv head) are dealt round-robin over its
+// TW = n_splits * WAVES waves: wave gw takes tiles gw, gw + TW, gw + 2*TW, ...
+// (the reference also interleaves 16-row blocks over its P programs,
+// kernels/decode_attention.py:71-75).  A wave keeps the G query heads of its
+// kv head as MFMA columns (attn_engine.h); the waves of a workgroup fold their
+// softmax states through LDS.  With one split the workgroup writes o
+// directly.  Otherwise it writes a partial (m, l, acc) per head, and the last
+// workgroup of the (sequence, kv head) to finish — elected on a device-scope
+// arrival counter (arrive_last) — merges the splits with log-sum-exp as
+// kernels/decode_attention.py:243-264 does, writes o and resets the counter
+// to zero for the next call.
 #include "attn_engine.h"
 
 // Build-time tuning (defaults are the shipped configuration):
 //   CIE_DECODE_WAVES  wavefronts per workgroup
 //   CIE_DECODE_PF     32-key steps whose loads are in flight ahead of the math
-//   CIE_DECODE_MERGE  how the splits meet: 2 = last-arriver with agent-scope
-//                     (sc1) partial stores / loads, 1 = last-arriver with
-//                     release / acquire fences, 3 = a second merge launch
 #ifndef CIE_DECODE_WAVES
 #define CIE_DECODE_WAVES 4
 #endif
 #ifndef CIE_DECODE_PF
 #define CIE_DECODE_PF 1
-#endif
-#ifndef CIE_DECODE_MERGE
-#define CIE_DECODE_MERGE 2
 #endif
 
 namespace cie {
@@ -68,7 +63,7 @@ struct DecodeParams {
   float* part_m;    // (B, H_q, S)
   float* part_l;    // (B, H_q, S)
   float* part_acc;  // (B, H_q, S, D)
-  int32_t* counters;  // (B * H_kv), zero between calls
+  int32_t* counters;  // 2 * (B * H_kv): arrival words, then stale words; zero between calls
   int64_t pool_page_stride, pool_head_stride, bt_stride, n_pages;
   int32_t bt_width, n_slots, B, H_q, H_kv, G, page_size, n_splits;
   float scale_log2;
@@ -188,23 +183,11 @@ __device__ __forceinline__ void put_new_k(KVPair<D>& kv, int key0a, int key0b, i
   }
 }
 
-// Split partials cross workgroups (and XCDs, each with its own L2).  With the
-// fence-free merge they are written and read as agent-scope atomics
-// (global_store / global_load ... sc1), coherent device-wide.
-__device__ __forceinline__ void partial_store(float* ptr, float v) {
-#if CIE_DECODE_MERGE == 2
-  __hip_atomic_store(ptr, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  *ptr = v;
-#endif
-}
-__device__ __forceinline__ float partial_load(const float* ptr) {
-#if CIE_DECODE_MERGE == 2
-  return __hip_atomic_load(const_cast<float*>(ptr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#else
-  return *ptr;
-#endif
-}
+// Split partials cross workgroups (and XCDs, each with its own L2): they are
+// written and read only as agent-scope atomics (global_store / global_load /
+// buffer accesses with sc1), coherent device-wide (arrive_last).
+__device__ __forceinline__ void partial_store(float* ptr, float v) { agent_store(ptr, v); }
+__device__ __forceinline__ float partial_load(const float* ptr) { return agent_load(ptr); }
 
 constexpr int kMaxSplits = 64;
 
@@ -212,17 +195,17 @@ template <int D, int NTHREADS>
 __device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g);
 
 // Profiling builds only (-DCIE_DECODE_TRACE): wave 0 of every workgroup
-// stamps phase boundaries (s_memrealtime) into the buffer passed as `err`.
-// A stamp waits for nothing but its own clock read.
+// stamps phase boundaries (s_memrealtime) into a trace buffer of its own,
+// named by cie_decode_trace_buffer() (exported by such builds alone), 24
+// words per workgroup.  A stamp waits for nothing but its own clock read.
 #ifdef CIE_DECODE_TRACE
 constexpr int kTraceSlots = 24;
-#define DECODE_TRACE_LANE0(k, v)                                                          \
-  do {                                                                                    \
-    if ((threadIdx.x & (kWave - 1)) == 0 && p.err != nullptr) {                         \
-      reinterpret_cast<uint64_t*>(p.err)[((int64_t)(b * p.H_kv + g) * p.n_splits + split) * \
-                                             kTraceSlots +                                \
-                                         (k)] = (v);                                      \
-    }                                                                                     \
+__device__ uint64_t* g_decode_trace;
+#define DECODE_TRACE_LANE0(k, v)                                                               \
+  do {                                                                                         \
+    if ((threadIdx.x & (kWave - 1)) == 0 && g_decode_trace != nullptr) {                     \
+      g_decode_trace[((int64_t)(b * p.H_kv + g) * p.n_splits + split) * kTraceSlots + (k)] = (v); \
+    }                                                                                          \
   } while (0)
 #define DECODE_TRACE(k, v)                  \
   do {                                      \
@@ -534,36 +517,14 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   DECODE_TRACE(9, __builtin_amdgcn_s_memrealtime());
   if (S == 1) return;
 
-#if CIE_DECODE_MERGE != 3
-  // Last workgroup of this (sequence, kv head) to arrive merges the splits.
-#if CIE_DECODE_MERGE == 2
-  // Partials went out as agent-scope (sc1) stores; once they have completed
-  // (vmcnt 0) they are visible device-wide, so no L2 writeback is needed
-  // before the arrival count.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // s_waitcnt vmcnt(0)
-  DECODE_TRACE(3, __builtin_amdgcn_s_memrealtime());
-  __syncthreads();
-  if (threadIdx.x == 0)
-    sm_last = __hip_atomic_fetch_add(&p.counters[b * p.H_kv + g], 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT) == S - 1;
-  __syncthreads();
+  // The last workgroup of this (sequence, kv head) to arrive merges the splits.
+  int32_t* const arrival = p.counters + b * p.H_kv + g;
+  const bool last = arrive_last(arrival, (int64_t)p.B * p.H_kv, S, &sm_last, p.err);
   DECODE_TRACE(10, __builtin_amdgcn_s_memrealtime());
-  if (!sm_last) return;
-#else
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    sm_last = __hip_atomic_fetch_add(&p.counters[b * p.H_kv + g], 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT) == S - 1;
-  }
-  __syncthreads();
-  if (!sm_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-#endif
+  if (!last) return;
   merge_splits<D, WAVES * kWave>(p, b, g);
-  if (threadIdx.x == 0) p.counters[b * p.H_kv + g] = 0;
+  if (threadIdx.x == 0) counter_reset(arrival);
   DECODE_TRACE(4, __builtin_amdgcn_s_memrealtime());
-#endif
 }
 
 // Combine the S partial states of every head of (b, g) into o.  A thread
@@ -625,12 +586,6 @@ __device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g
   }
 }
 
-// Separate merge launch (CIE_DECODE_MERGE == 3): one workgroup per (g, b).
-template <int D>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
-  merge_splits<D, 256>(p, blockIdx.y, blockIdx.x);
-}
-
 // Waves per workgroup: four, one per SIMD.  With the non-temporal K/V loads
 // a 4-wave workgroup per CU streams faster than an 8-wave one (config 2:
 // 16.99 vs 18.08 us per call): the second wave per SIMD only queued more
@@ -670,16 +625,8 @@ static int launch_decode(const DecodeParams& p, hipStream_t stream) {
   constexpr int W = decode_waves<D>();
   constexpr int Wh = W > 4 ? W / 2 : W;
   const int64_t n_wg = (int64_t)p.n_splits * p.H_kv * p.B;
-  int rc = (Wh != W && n_wg > device_cus())
-               ? launch_decode_waves<D, Wh, kAppend, kRope>(p, stream)
-               : launch_decode_waves<D, W, kAppend, kRope>(p, stream);
-#if CIE_DECODE_MERGE == 3
-  if (rc == 0 && p.n_splits > 1) {
-    hipLaunchKernelGGL((decode_merge_kernel<D>), dim3(p.H_kv, p.B), dim3(256), 0, stream, p);
-    rc = (int)hipGetLastError();
-  }
-#endif
-  return rc;
+  return (Wh != W && n_wg > device_cus()) ? launch_decode_waves<D, Wh, kAppend, kRope>(p, stream)
+                                          : launch_decode_waves<D, W, kAppend, kRope>(p, stream);
 }
 
 // Partials buffer: part_m | part_l | part_acc (fp32), each region 256-byte aligned.
@@ -758,6 +705,15 @@ extern "C" int64_t cie_paged_decode_partials_bytes(int64_t B, int64_t H_q, int64
 }
 
 extern "C" int cie_paged_decode_max_splits(void) { return kMaxSplits; }
+
+#ifdef CIE_DECODE_TRACE
+// Trace builds only: where the decode kernels stamp their phases (device
+// buffer of 24 uint64 per workgroup; NULL turns the stamps off).
+extern "C" int cie_decode_trace_buffer(void* buf) {
+  uint64_t* p = static_cast<uint64_t*>(buf);
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_decode_trace), &p, sizeof(p));
+}
+#endif
 
 extern "C" int cie_paged_decode(void* o, const void* q, const void* k_pool, const void* v_pool,
                                 const int64_t* lens, const int64_t* slot_ids,

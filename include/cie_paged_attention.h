@@ -39,6 +39,8 @@ extern "C" {
 #define CIE_ERRBIT_PAGE 1     /* page id outside [0, n_pages)                    */
 #define CIE_ERRBIT_LEN 2      /* length beyond the block-table row capacity      */
 #define CIE_ERRBIT_OFFSET 4   /* in-page offset outside [0, page_size)           */
+#define CIE_ERRBIT_SPLIT 8    /* a split-arrival counter held a stale value at the
+                                 start of the call (see `counters` below)        */
 
 /* Version of this ABI (bumped on any signature change). */
 int cie_abi_version(void);
@@ -97,11 +99,16 @@ int cie_kv_append_tokens(void* k_pool, void* v_pool,
  *                (1 <= n_splits <= cie_paged_decode_max_splits())
  *   partials   : cie_paged_decode_partials_bytes(B, H_q, D, n_splits) bytes,
  *                16-byte aligned, any contents: the splits' softmax state
- *   counters   : B * H_kv int32, 16-byte aligned: one arrival counter per
- *                (sequence, kv head).  They must be zero before the call and
- *                every completed call leaves them zero, so one zeroed buffer
- *                serves any number of stream-ordered calls.  Calls that can
- *                overlap in time must not share counters or partials.
+ *   counters   : 2 * B * H_kv int32, 16-byte aligned: one arrival word per
+ *                (sequence, kv head), then one stale word per (sequence, kv
+ *                head).  They must be zero before the call and every
+ *                completed call leaves them zero, so one zeroed buffer serves
+ *                any number of stream-ordered calls.  Calls that can overlap
+ *                in time must not share counters or partials.  A call that
+ *                finds an arrival word outside [0, n_splits) raises
+ *                CIE_ERRBIT_SPLIT (its o is then not valid); when every split
+ *                of a (sequence, kv head) finds it stale, the call also puts
+ *                both words back to zero.
  *   partials and counters may be NULL when n_splits == 1.
  */
 int64_t cie_paged_decode_partials_bytes(int64_t B, int64_t H_q, int64_t D,
@@ -204,9 +211,10 @@ int cie_kv_append_tokens_qkv_rope(void* q_out, void* k_pool, void* v_pool,
  *   partials   : cie_mixed_partials_bytes(total_T, H_q, D) bytes, 16-byte
  *                aligned, any contents (per-chunk softmax state)
  *   counters   : cie_mixed_counters(B, H_kv, max_seqlen) int32, 16-byte
- *                aligned, zero before the call and left zero by it (one
- *                arrival counter per query tile and column group; the same
- *                buffer can serve cie_paged_decode, calls being
+ *                aligned, zero before the call and left zero by it (an
+ *                arrival word and a stale word per query tile and column
+ *                group, with CIE_ERRBIT_SPLIT as for cie_paged_decode; the
+ *                same buffer can serve cie_paged_decode, calls being
  *                stream-ordered)
  */
 int64_t cie_mixed_partials_bytes(int64_t total_T, int64_t H_q, int64_t D);
@@ -222,18 +230,6 @@ int cie_mixed_attention(void* o, const void* q,
                         int64_t pool_page_stride, int64_t pool_head_stride,
                         int64_t bt_stride, int64_t bt_width, int64_t n_slots,
                         int32_t* err, void* stream);
-
-/*
- * Measurement helper, no counterpart in the reference: reads n_chunks chunks
- * of chunk_bytes (1024, 2048 or 4096) at base + chunk_ids[i] * chunk_bytes and
- * folds them into *sink (written only on an improbable hash), on
- * n_workgroups workgroups of 256 threads.  Timed with shuffled ids and the KV
- * page-head size it gives the HBM ceiling of the paged access pattern,
- * without any attention math; bench.py reports it beside the decode figure.
- */
-int cie_probe_gather_read(const void* base, const int32_t* chunk_ids,
-                          int64_t n_chunks, int64_t chunk_bytes,
-                          int64_t n_workgroups, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,99 @@
+"""The split merge's ordering, checked in this build's own gfx950 assembly (CPU).
+
+The decode and mixed kernels publish a split's partial state with agent-scope
+(sc1) stores and then count the split in with a relaxed agent-scope
+``fetch_add`` (``arrive_last`` in csrc/cie_common.h).  Nothing in the HIP
+memory model orders relaxed stores before a relaxed RMW, so the kernels rely
+on the hardware order: every store has completed (``s_waitcnt vmcnt(0)``)
+before the atomic is issued, and the merging workgroup reads the partials
+only with sc1 loads issued after the atomic returned.  This test compiles the
+kernel sources to gfx950 assembly with the library's own flags and checks, in
+every kernel that elects a last arriver, that
+
+  * the arrival atomic (the first returning ``global_atomic_add``) has a
+    ``s_waitcnt`` with ``vmcnt(0)`` after the last vector-memory store before it;
+  * every store of the partial state carries sc1, and no L2 writeback or
+    invalidate (``buffer_wbl2`` / ``buffer_inv``) is emitted;
+  * the merge's partial loads (sc1 loads after the atomic) come after a
+    ``vmcnt(0)`` wait on the atomic's result.
+"""
+from __future__ import annotations
+
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from custom_inference_engine_amd import _build
+
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+pytestmark = pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not available")
+
+STORE = re.compile(r"^\s*(global|buffer|flat)_store\w*")
+ATOMIC_RET = re.compile(r"^\s*global_atomic_add\b.*\bsc0\b")
+WAIT_VM0 = re.compile(r"^\s*s_waitcnt\b.*\bvmcnt\(0\)")
+SC1_LOAD = re.compile(r"^\s*(global|buffer)_load\w*.*\bsc1\b")
+
+
+def _assembly(src: str, tmp_path) -> str:
+    out = tmp_path / (os.path.basename(src) + ".s")
+    flags = [f for f in _build.HIPCC_FLAGS if f != "-fPIC"]
+    cmd = [HIPCC, *flags, "-I", _build.INCLUDE, "-I", _build.CSRC, "--offload-device-only", "-S",
+           os.path.join(_build.CSRC, src), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-4000:]
+    return out.read_text()
+
+
+def _kernels(asm: str) -> dict[str, list[str]]:
+    """Kernel symbol -> its instruction lines (label to .Lfunc_end)."""
+    out, name, body = {}, None, []
+    for line in asm.splitlines():
+        m = re.match(r"^(_Z\w+):", line)
+        if m:
+            name, body = m.group(1), []
+            continue
+        if name is not None:
+            if line.startswith(".Lfunc_end"):
+                out[name] = body
+                name = None
+            else:
+                body.append(line)
+    return out
+
+
+def _check_arrival(name: str, body: list[str]) -> None:
+    atom = next((i for i, l in enumerate(body) if ATOMIC_RET.match(l)), None)
+    assert atom is not None, f"{name}: no arrival atomic"
+    waited = False
+    for line in reversed(body[:atom]):
+        if WAIT_VM0.match(line):
+            waited = True
+        if STORE.match(line):
+            assert waited, f"{name}: a store before the arrival atomic is not waited for: {line.strip()}"
+            break
+    else:
+        pytest.fail(f"{name}: no partial store before the arrival atomic")
+    # the merge reads partials with sc1 loads, after waiting for the atomic's value
+    later = body[atom + 1:]
+    first_load = next((i for i, l in enumerate(later) if SC1_LOAD.match(l)), None)
+    assert first_load is not None, f"{name}: no sc1 partial loads after the arrival"
+    assert any(WAIT_VM0.match(l) for l in later[:first_load]), \
+        f"{name}: partial loads issued before the arrival atomic returned"
+
+
+@pytest.mark.parametrize("src,kernel", [("paged_decode.hip", "decode_kernel"),
+                                         ("mixed_attention.hip", "mixed_attention_kernel")])
+def test_partials_complete_before_arrival(src, kernel, tmp_path):
+    asm = _assembly(src, tmp_path)
+    assert "buffer_wbl2" not in asm and "buffer_inv" not in asm
+    kernels = {n: b for n, b in _kernels(asm).items() if kernel in n}
+    assert kernels, f"no {kernel} in the assembly"
+    for name, body in kernels.items():
+        _check_arrival(name, body)
+        # partial stores are agent-scope: every store of the merge path carries sc1,
+        # except the output o (plain global stores of fp16) and the pool append
+        partial_stores = [l for l in body if STORE.match(l) and "dwordx4" in l and "buffer_store" in l]
+        assert partial_stores and all("sc1" in l for l in partial_stores), name

@@ -152,7 +152,7 @@ def test_decode_counters_return_to_zero(native_lib):
     note("split counters")
     c = case.to(DEV)
     kp, vp = (t.to(DEV) for t in case.appended_pools())
-    ctr = torch.zeros(case.B * 2, dtype=torch.int32, device=DEV)
+    ctr = torch.zeros(2 * case.B * 2, dtype=torch.int32, device=DEV)  # arrival + stale words
     outs = []
     for splits in (7, 7, 3, 16):
         o = decode_gqa_attention(c.q, kp, vp, c.attended, c.slot_ids, c.block_table,
@@ -163,3 +163,35 @@ def test_decode_counters_return_to_zero(native_lib):
     assert torch.equal(outs[0], outs[1])
     for o in outs:
         assert_attn_close(o[0].float().cpu(), oracle_decode(case), what="counters")
+
+
+def test_decode_stale_counter_is_flagged_and_cleared(native_lib):
+    """An arrival word left at n_splits or more (a caller's unzeroed buffer) raises
+    CIE_ERRBIT_SPLIT; every split of that (sequence, kv head) sees it stale, so the
+    call puts the word back to zero and the next call is correct again.  The other
+    (sequence, kv head) groups of the stale call are unaffected."""
+    case = inputs.make_case([300, 1, 2000], seed=31)
+    note("decode stale counter")
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    want = oracle_decode(case)
+    S, n = 4, case.B * 2
+    ctr = torch.zeros(2 * n, dtype=torch.int32, device=DEV)
+    ctr[2 * 1 + 1] = S + 5  # arrival word of (sequence 1, kv head 1)
+    err = err_word()
+    o = decode_gqa_attention(c.q, kp, vp, c.attended, c.slot_ids, c.block_table, num_programs=S,
+                             counters=ctr, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 8, "CIE_ERRBIT_SPLIT expected"
+    assert torch.count_nonzero(ctr) == 0, ctr.tolist()
+    fine = [(b, h) for b in range(case.B) for h in range(14) if not (b == 1 and h >= 7)]
+    got = o[0].float().cpu()
+    for b, h in fine:
+        assert_attn_close(got[b, h], want[b, h], what=f"untouched group b={b} h={h}")
+    err.zero_()
+    o = decode_gqa_attention(c.q, kp, vp, c.attended, c.slot_ids, c.block_table, num_programs=S,
+                             counters=ctr, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert torch.count_nonzero(ctr) == 0
+    assert_attn_close(o[0].float().cpu(), want, what="call after the stale one")

@@ -202,3 +202,31 @@ def test_mixed_counters_return_to_zero(native_lib):
         torch.cuda.synchronize()
         assert torch.count_nonzero(ctr) == 0
     _check(case, o[0].float().cpu(), "mixed counters")
+
+
+def test_mixed_stale_counters_are_flagged_and_cleared(native_lib):
+    """Arrival words preloaded far above any chunk count raise CIE_ERRBIT_SPLIT in a
+    call with multi-chunk tiles; every chunk of those tiles sees its word stale, so the
+    call clears the words it uses and the next call is correct with no error bit."""
+    case = inputs.make_case([6000, 0, 2500, 700, 30000], [40, 1, 1, 18, 1], seed=37)
+    note("mixed stale counters")
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    from custom_inference_engine_amd import mixed_gqa_attention
+    n = _native.load().cie_mixed_counters(case.B, 2, 40)
+    ctr = torch.zeros(n, dtype=torch.int32, device=DEV)
+    ctr[: n // 2] = 1000  # every arrival word
+    err = err_word()
+    mixed_gqa_attention(c.q, kp, vp, 40, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
+                        counters=ctr, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 8, "CIE_ERRBIT_SPLIT expected"
+    assert torch.count_nonzero(ctr[n // 2:]) == 0  # stale words back to zero
+    used = ctr[: n // 2] == 0
+    assert bool(used.any())
+    err.zero_()
+    o = mixed_gqa_attention(c.q, kp, vp, 40, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
+                            counters=ctr, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    _check(case, o[0].float().cpu(), "call after the stale one")
