@@ -101,16 +101,9 @@ def time_calls(fn_list, steps: int, warmup: int, use_graph: bool, repeats: int) 
             f()
 
     if use_graph:
-        side = torch.cuda.Stream()
-        side.wait_stream(stream)
-        with torch.cuda.stream(side):
-            run_all()
-        stream.wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            run_all()
-        body = graph.replay
+        from custom_inference_engine_amd.graphs import StepGraph
+
+        body = StepGraph(run_all).replay
     else:
         body = run_all
     for _ in range(max(1, -(-warmup // R))):
@@ -640,7 +633,7 @@ def bench_model(args, cie, dev, n_requests: int = 64, n_slots: int = 33, new_tok
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for _ in range(n_rep):
-            dec.graph.replay()
+            dec.step.replay()
         end.record()
         torch.cuda.synchronize()
         replay_us = start.elapsed_time(end) * 1e3 / n_rep

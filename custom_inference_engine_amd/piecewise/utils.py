@@ -1,14 +1,15 @@
 """Graph surgery for the piecewise backend (piecewise/utils.py:5-62 of the reference).
 
 Dynamo hands the backend the FX graph of a whole mixed step.  Its varlen
-attention calls (``inference::gqa_mixed_attention``) depend on the batch's
-per-sequence tensors, whose sizes change from step to step; everything
-between them (projections, norms, MLPs, the KV append) has the token
-bucket's fixed shapes.  The graph is therefore cut around each attention
-node — together with the node that gathers its ``kv_lens`` argument, which
-also reads the per-sequence ``slot_ids`` — into alternating pieces: the
-even-numbered ones hold no attention and can be replayed from a hipGraph,
-the odd-numbered ones run eagerly.
+attention calls (``inference::gqa_mixed_attention``) read the batch's
+per-sequence tensors; everything between them (projections, norms, MLPs,
+the KV append) reads only per-token tensors of the token bucket's shape.
+The graph is cut around each attention node — together with the node that
+gathers its ``kv_lens`` argument, which also reads the per-sequence
+``slot_ids`` — into alternating pieces: the even-numbered ones hold no
+attention and are replayed from hipGraphs, the odd-numbered ones run
+eagerly.  Which nodes go where is the reference's rule, kept because the
+pieces' inputs (what a recorded graph may read) follow from it.
 """
 from __future__ import annotations
 

@@ -1,15 +1,15 @@
-"""Step modules around the attention path, mirroring the reference's scheduler/ layout.
+"""Step modules and continuous batching around the attention path.
 
-``DecodeModule`` (scheduler/decode_module.py:8-107 of the reference) captures a
-whole decode step of the model — every layer's fused KV append + paged decode —
-in one hipGraph per batch bucket and replays it; ``MixedModule``
-(scheduler/mixed_module.py:10-133) runs a packed chunked-prefill / decode
-step eagerly and ``FullMixedModule`` (scheduler/mixed_module.py:164-213)
-replays it from a hipGraph per token bucket; ``PiecewiseMixedModule``
-(scheduler/mixed_module.py:216-249) compiles it through the piecewise backend
-(hipGraph pieces between eager varlen attention calls); ``Scheduler`` (scheduler/scheduler.py) is the continuous-batching
-policy around them (token budget, chunked prefill, page allocation, recompute
-preemption).
+``DecodeModule`` replays a whole-model decode step from one hipGraph per batch
+bucket; ``MixedModule`` / ``FullMixedModule`` / ``PiecewiseMixedModule`` run a
+packed chunked-prefill / decode step eagerly, from one hipGraph per token
+bucket, or compiled through the piecewise backend (hipGraph pieces between
+eager varlen attention calls).  All of them take their per-step inputs as one
+pinned block copied in one transfer and derive the step's metadata on the
+device (``graphs.StepInputs`` / ``graphs.StepGraph``).  ``Scheduler``
+(scheduler/scheduler.py of the reference) is the continuous-batching policy
+around them: token budget, chunked prefill, page allocation, recompute
+preemption.
 """
 from .decode_module import DecodeModule  # noqa: F401
 from .mixed_module import FullMixedModule, MixedModule, PiecewiseMixedModule  # noqa: F401

@@ -1,78 +1,82 @@
-"""One decode step of the whole model, captured in a hipGraph per batch bucket.
+"""Whole-model decode steps replayed from one hipGraph per batch bucket.
 
-Mirrors scheduler/decode_module.py:8-107 of the reference: static ``(1, B)``
-token and position buffers, a full-decode ``AttentionMetadata``, warmup runs
-on a side stream, one graph capture of the step (the model forward — whose
-attention layers run the fused KV append + paged decode — plus
-``decode_advance``), then ``upload`` / ``replay`` / argmax per step.  The
-reference compiles the forward with ``torch.compile`` before capture; here the
-eager forward is captured as is (the attention path is already one HIP launch
-per layer, and the rest of the layer is library GEMMs and elementwise ops).
+Serves the decode steps of the reference's engine (one token per running
+sequence; the reference's DecodeModule, scheduler/decode_module.py:8-107, is
+the interface kept: constructor arguments, ``forward(slot_ids) -> next tokens``).
+
+Design.  The only per-step input is the bucket's slot list (padded with the
+reserved slot 0).  Everything else a step needs is already on the device and
+is read inside the graph: the input token of sequence b is
+``kv_cache.last_generated[slot_b]`` and its position is ``kv_cache.lens[slot_b]``
+(two gathers recorded in the graph), the attention layers append and attend
+through the fused decode kernel, ``decode_advance`` moves the lengths on, and
+the LM head produces the bucket's logits.  A step is therefore: write the slot
+ids into a pinned block, one asynchronous copy, one graph replay, then the
+argmax and the ``last_generated`` update (kept out of the graph: argmax over a
+151,936-wide vocabulary is a multi-block library reduction, and such library
+kernels are not recorded) and one device-to-host copy of the tokens.
+
+The capture's warm-up runs the step on the initial all-padding slot list, so it
+touches only slot 0 and page 0 (reserved; ``decode_advance`` keeps slot 0's
+length at zero): no real slot is used or has to be reset afterwards.
 """
 from __future__ import annotations
 
 import torch
 
 from ..attn.metadata import AttentionMetadata
-from .slots import pad_slot_ids
+from ..graphs import StepGraph, StepInputs
 
 
 class DecodeModule:
     def __init__(self, model, kv_cache, batch_size: int, pool=None, warmup_iters: int = 3):
         self.model = model
-        self.batch_size = batch_size
         self.kv_cache = kv_cache
-        device = model.device
-        self.device = device
+        self.batch_size = batch_size
+        self.device = model.device
+        dev = self.device
 
-        self.metadata = AttentionMetadata(token_count=batch_size, device=device, full_decode=True)
-        self.metadata.prepare_full_graph(batch_size)
-
+        self.inputs = StepInputs(dev, slots=batch_size)
+        self.inputs.host("slots")[:] = kv_cache.unused_idx
+        self.inputs.upload()
+        self.slots = self.inputs.device("slots")
+        self.metadata = AttentionMetadata(token_count=batch_size, device=dev, full_decode=True)
+        self.metadata.slot_ids = self.slots
+        self.tokens = torch.zeros((batch_size,), dtype=torch.long, device=dev)
+        self.positions = torch.zeros((batch_size,), dtype=torch.long, device=dev)
         with torch.inference_mode():
-            self.static_token = torch.zeros((1, batch_size), device=device, dtype=torch.long)
-            self.static_position_ids = torch.zeros((1, batch_size), device=device, dtype=torch.long)
+            self.step = StepGraph(self._step, pool=pool, warmup=warmup_iters, device=dev)
+        self.logits = self.step.output  # (batch_size, vocab), rewritten by every replay
 
-            side = torch.cuda.Stream(device=device)
-            side.wait_stream(torch.cuda.current_stream(device))
-            with torch.cuda.stream(side):
-                for _ in range(max(1, warmup_iters)):
-                    self._forward()
-            torch.cuda.current_stream(device).wait_stream(side)
-            torch.cuda.synchronize(device)
-
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph, pool=pool):
-                self.static_logits = self._forward().logits[0]
-        self.warmup()
-
-    def warmup(self) -> None:
-        slot_ids = list(range(1, min(self.batch_size, self.kv_cache.n_slots - 1) + 1))
-        self.forward(slot_ids)
-        self.kv_cache.reset(slot_ids)
-
-    def _forward(self):
-        outputs = self.model(input_ids=self.static_token, position_ids=self.static_position_ids,
-                             kv_manager=self.kv_cache, logits_to_keep=0, use_cache=False,
-                             metadata=self.metadata)
-        self.kv_cache.decode_advance(slot_ids=self.metadata.slot_ids)
-        return outputs
+    def _step(self) -> torch.Tensor:
+        kv = self.kv_cache
+        torch.index_select(kv.last_generated, 0, self.slots, out=self.tokens)
+        torch.index_select(kv.lens, 0, self.slots, out=self.positions)
+        hidden = self.model.model(input_ids=self.tokens[None], position_ids=self.positions[None],
+                                  kv_manager=kv, use_cache=False,
+                                  metadata=self.metadata).last_hidden_state
+        kv.decode_advance(slot_ids=self.slots)
+        return self.model.lm_head(hidden[0])
 
     def upload(self, slot_ids: list[int]) -> None:
-        padded = pad_slot_ids(slot_ids, self.batch_size, self.kv_cache.unused_idx)
-        self.static_position_ids.copy_(self.kv_cache.lens[padded][None])
-        self.static_token.copy_(self.kv_cache.last_generated[padded][None])
-        self.metadata.write_slot_ids(slot_ids)
+        n = len(slot_ids)
+        if n > self.batch_size:
+            raise ValueError(f"{n} sequences do not fit the decode bucket of {self.batch_size}")
+        host = self.inputs.host("slots")
+        host[:n] = slot_ids
+        host[n:] = self.kv_cache.unused_idx
+        self.inputs.upload()
 
     def replay(self) -> torch.Tensor:
-        self.graph.replay()
-        return self.static_logits
+        return self.step.replay()
 
     def forward(self, slot_ids: list[int]) -> list[int]:
-        if not slot_ids:
+        n = len(slot_ids)
+        if n == 0:
             return []
         with torch.inference_mode():
             self.upload(slot_ids)
             logits = self.replay()
-            next_tokens = torch.argmax(logits, dim=-1)[:len(slot_ids)]
-            self.kv_cache.last_generated[slot_ids] = next_tokens
-        return next_tokens.tolist()
+            next_tokens = torch.argmax(logits[:n], dim=-1)
+            self.kv_cache.last_generated[self.slots[:n]] = next_tokens
+            return next_tokens.tolist()

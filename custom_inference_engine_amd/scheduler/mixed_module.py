@@ -1,182 +1,198 @@
-"""A packed chunked-prefill step, after scheduler/mixed_module.py of the reference.
+"""Packed chunked-prefill / decode steps over the paged pool.
 
-``upload`` builds the step's metadata exactly as the reference does
-(scheduler/mixed_module.py:76-133): per-token slot ids, positions
-``lens[slot] + offset``, pages ``block_table[slot, pos // P]`` and offsets
-``pos % P``, ``cu_seqlens`` from the chunk lengths; ``forward`` runs the
-model's decoder stack (each attention layer: rope + token-mode KV append +
-varlen mixed attention), advances ``lens`` by the chunk lengths and returns
-the argmax token of each sequence's last row.
+Serves the mixed steps of the reference's engine: a batch of sequences, each
+feeding a chunk of new tokens (a prompt piece, or one decode token), packed
+into one token bucket.  The public surface is the reference's
+(scheduler/mixed_module.py:10-249: ``MixedModule(model, kv_cache,
+token_count)``, ``FullMixedModule(..., batch_size, token_count, pool)``,
+``PiecewiseMixedModule(..., token_count, buffer, pool)``, and
+``forward(prompts, slot_ids) -> next token per sequence``); the design below
+is this build's own.
 
-``MixedModule`` runs the step eagerly.  ``FullMixedModule`` captures the
-decoder stack of one token bucket in a hipGraph, like the reference's
-``FullMixedModule`` (scheduler/mixed_module.py:164-213): the batch is padded to
-a fixed number of sequences with the reserved slot and zero-length chunks
-(``cu_seqlens`` padded with its last value), pages / offsets with page 0, and
-``max_seqlen`` is the token bucket; the varlen kernel plans its work on the
-device, so padded sequences cost nothing.
+Design.  A step's host inputs are three fixed-size int64 vectors in one pinned
+block (``StepInputs``): the batch's slot ids and chunk lengths, padded to the
+module's batch capacity with slot 0 and length 0, and the packed token ids,
+padded to the token bucket with 0.  One asynchronous copy moves them.
+Everything else is derived on the device by ``_prepare`` (fixed shapes, in
+place into static buffers, so it can be recorded in a graph): ``cu_seqlens``
+by a cumulative sum of the lengths; the sequence of each packed row by a
+binary search in ``cu_seqlens``; its position ``lens[slot] + offset in its
+chunk``, page ``block_table[slot, pos // page_size]`` and in-page offset; rows
+past the batch's tokens get slot 0, position 0, page 0, offset 0 (the
+reserved padding targets).  Padded sequences have zero query rows, which the
+varlen kernel skips at no cost (it plans its work on the device), so one
+token bucket serves every batch size.  After the decoder stack, ``_advance``
+moves each slot's length on by its chunk and ``_logits`` applies the LM head
+to each sequence's last row; the argmax and the ``last_generated`` update
+run after the step, as in the decode module.
 
-``PiecewiseMixedModule`` is the reference's module for its larger token
-buckets (scheduler/mixed_module.py:216-249): ``torch.compile`` of the stack
-(``fullgraph=True``, ``dynamic=False``, the batch dimension of ``slot_ids`` and
-``cu_seqlens`` marked dynamic) through the piecewise backend, which replays the
-code between attention calls from hipGraphs and runs the varlen attention
-eagerly into a shared buffer; the batch is not padded.  Here one full graph
-per token bucket already covers every batch size, so the scheduler uses the
-piecewise module only when asked to.
+Three ways to run the same step:
+  * ``MixedModule``: everything eagerly.
+  * ``FullMixedModule``: ``_prepare``, the decoder stack, ``_advance`` and
+    ``_logits`` recorded in one hipGraph per token bucket (``StepGraph``);
+    its warm-up runs on the all-padding inputs, which touch only slot 0 and
+    page 0.
+  * ``PiecewiseMixedModule``: the decoder stack compiled with
+    ``torch.compile(fullgraph=True)`` through the piecewise backend (graph
+    pieces between eagerly run attention calls); ``_prepare``, ``_advance``
+    and ``_logits`` run eagerly.  All inputs have fixed shapes, so each token
+    bucket compiles exactly once (no dynamic dimensions).
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
-import torch.nn.functional as F
 
 from ..attn.metadata import AttentionMetadata
+from ..graphs import StepGraph, StepInputs
 from ..piecewise import get_piecewise_backend
-from .slots import pad_slot_ids
 
 
 class MixedModule:
-    def __init__(self, model, kv_cache, token_count: int):
+    def __init__(self, model, kv_cache, token_count: int, batch_size: int | None = None):
         self.model = model
         self.kv_cache = kv_cache
         self.token_count = token_count
+        self.batch_size = batch_size or max(1, kv_cache.n_slots - 1)
         self.device = model.device
-        self.metadata = AttentionMetadata(token_count=token_count, device=self.device, full_decode=False)
-        self.lens = None
-        self.last_logits = None  # (B, vocab) of the last forward
-        with torch.inference_mode():
-            self.static_input_ids = torch.zeros((1, token_count), device=self.device, dtype=torch.long)
-            self.static_position_ids = torch.zeros((1, token_count), device=self.device, dtype=torch.long)
+        dev, B, T = self.device, self.batch_size, token_count
 
-    # -- hooks: how the batch's per-sequence tensors reach the metadata, and how the stack runs
+        self.inputs = StepInputs(dev, slots=B, chunk_lens=B, tokens=T)
+        self.slots = self.inputs.device("slots")
+        self.chunk_lens = self.inputs.device("chunk_lens")
+        self.tokens = self.inputs.device("tokens")
+        self.inputs.host("slots")[:] = kv_cache.unused_idx
+        self.inputs.upload()
+        self.cu_seqlens = torch.zeros((B + 1,), dtype=torch.long, device=dev)
+        self.positions = torch.zeros((T,), dtype=torch.long, device=dev)
+        self.rows = torch.arange(T, dtype=torch.long, device=dev)
+        self.metadata = AttentionMetadata(token_count=T, device=dev, full_decode=False)
+        self.metadata.slot_ids = self.slots
+        self.metadata.cu_seqlens = self.cu_seqlens
+        self.metadata.max_seqlen = T
+        self.last_logits = None  # (n, vocab) of the last forward
 
-    def _pad(self, slot_ids: list[int]) -> list[int]:
-        return list(slot_ids)
+    # -- the step, in pieces
 
-    def _write_batch(self, slots: torch.Tensor, cu_seqlens: torch.Tensor, lens: torch.Tensor) -> None:
-        self.metadata.slot_ids = slots
-        self.metadata.cu_seqlens = cu_seqlens
-        self.lens = lens
+    def _prepare(self) -> None:
+        """cu_seqlens, positions, pages and offsets from (slots, chunk_lens)."""
+        kv, B = self.kv_cache, self.batch_size
+        torch.cumsum(self.chunk_lens, 0, out=self.cu_seqlens[1:])
+        seq = torch.searchsorted(self.cu_seqlens[1:], self.rows, right=True)
+        live = seq < B
+        seq.clamp_(max=B - 1)
+        slot = torch.where(live, self.slots[seq], kv.unused_idx)
+        pos = torch.where(live, kv.lens[slot] + (self.rows - self.cu_seqlens[seq]), 0)
+        self.positions.copy_(pos)
+        self.metadata.pages.copy_(torch.where(live, kv.block_table[slot, pos // kv.page_size], 0))
+        self.metadata.offsets.copy_(pos % kv.page_size)
 
     def _forward(self) -> torch.Tensor:
-        return self.model.model(input_ids=self.static_input_ids, position_ids=self.static_position_ids,
+        return self.model.model(input_ids=self.tokens[None], position_ids=self.positions[None],
                                 kv_manager=self.kv_cache, use_cache=False,
                                 metadata=self.metadata).last_hidden_state
 
-    def replay(self) -> torch.Tensor:
-        return self._forward()
+    def _advance(self) -> None:
+        self.kv_cache.mixed_advance(slot_ids=self.slots, lens=self.chunk_lens)
 
-    def warmup(self, n: int) -> None:
-        """One real step through slots 1..n (then reset), as the reference's warm-up does
-        (scheduler/mixed_module.py:41-47)."""
-        slot_ids = list(range(1, n + 1))
-        self.forward([[0] * (self.token_count // n) for _ in slot_ids], slot_ids)
-        self.kv_cache.reset(slot_ids)
+    def _logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        last = (self.cu_seqlens[1:] - 1).clamp(min=0)
+        return self.model.lm_head(hidden[0, last])
 
-    # -- the step
+    def _step(self) -> torch.Tensor:
+        self._prepare()
+        hidden = self._forward()
+        self._advance()
+        return self._logits(hidden)
+
+    def run(self) -> torch.Tensor:
+        """The step on the uploaded inputs; (batch_size, vocab) logits."""
+        return self._step()
+
+    # -- host side
 
     def upload(self, prompts: list[list[int]], slot_ids: list[int]) -> int:
         if len(prompts) != len(slot_ids):
             raise ValueError("len(prompts) must equal len(slot_ids).")
-        padded = self._pad(slot_ids)
-        lens_list = [len(p) for p in prompts] + [0] * (len(padded) - len(prompts))
-        total_T = sum(lens_list)
-        if total_T > self.token_count:
-            raise ValueError(f"{total_T} tokens exceed the step's budget of {self.token_count}")
-        dev = self.device
-        lens = torch.tensor(lens_list, dtype=torch.long, device=dev)
-        slots = torch.tensor(padded, dtype=torch.long, device=dev)
-        cu_seqlens = F.pad(lens.cumsum(0), (1, 0))
-        ext_slots = torch.repeat_interleave(slots, lens, output_size=total_T)
-        seq_off = torch.arange(total_T, device=dev) - torch.repeat_interleave(cu_seqlens[:-1], lens,
-                                                                              output_size=total_T)
-        pos = self.kv_cache.lens[ext_slots] + seq_off
-        ids = torch.tensor([t for p in prompts for t in p], dtype=torch.long, device=dev)
-        self.static_input_ids.zero_()
-        self.static_position_ids.zero_()
-        self.static_input_ids[0, :total_T] = ids
-        self.static_position_ids[0, :total_T] = pos
-        self.metadata.write_pages(self.kv_cache.block_table[ext_slots, pos // self.kv_cache.page_size])
-        self.metadata.write_offsets(pos % self.kv_cache.page_size)
-        self.metadata.max_seqlen = self.token_count
-        self._write_batch(slots, cu_seqlens, lens)
-        return total_T
+        n = len(slot_ids)
+        if n > self.batch_size:
+            raise ValueError(f"{n} sequences do not fit the step's batch of {self.batch_size}")
+        lens = [len(p) for p in prompts]
+        total = sum(lens)
+        if total > self.token_count:
+            raise ValueError(f"{total} tokens exceed the step's budget of {self.token_count}")
+        slots, chunk_lens, tokens = (self.inputs.host(k) for k in ("slots", "chunk_lens", "tokens"))
+        slots[:n] = slot_ids
+        slots[n:] = self.kv_cache.unused_idx
+        chunk_lens[:n] = lens
+        chunk_lens[n:] = 0
+        tokens[:total] = [t for p in prompts for t in p]
+        tokens[total:] = 0
+        self.inputs.upload()
+        return total
 
     def forward(self, prompts: list[list[int]], slot_ids: list[int]) -> list[int]:
-        """Prefill (a chunk of) each prompt into its slot; returns each sequence's next token."""
-        if not slot_ids:
+        """Feed each sequence its chunk; returns each sequence's next token (argmax of
+        its last row)."""
+        n = len(slot_ids)
+        if n == 0:
             return []
         with torch.inference_mode():
             self.upload(prompts, slot_ids)
-            # the whole token bucket runs, as in the reference: padding tokens
-            # append to the reserved page 0 and lie outside every sequence
-            hidden = self.replay()
-            self.kv_cache.mixed_advance(slot_ids=self.metadata.slot_ids, lens=self.lens)
-            rows = self.metadata.cu_seqlens[1:len(slot_ids) + 1] - 1
-            logits = self.model.lm_head(hidden[0, rows])
+            logits = self.run()[:n]
             self.last_logits = logits
             next_tokens = torch.argmax(logits, dim=-1)
-            self.kv_cache.last_generated[self.metadata.slot_ids[:len(slot_ids)]] = next_tokens
-        return next_tokens.tolist()
+            self.kv_cache.last_generated[self.slots[:n]] = next_tokens
+            return next_tokens.tolist()
 
 
 class FullMixedModule(MixedModule):
-    """The decoder stack of one token bucket, captured in a hipGraph (see the module docstring)."""
+    """The whole step of one token bucket replayed from a hipGraph."""
 
     def __init__(self, model, kv_cache, batch_size: int, token_count: int, pool=None,
                  warmup_iters: int = 3):
-        super().__init__(model, kv_cache, token_count)
-        self.batch_size = batch_size
-        self.metadata.prepare_full_graph(batch_size)
+        super().__init__(model, kv_cache, token_count, batch_size=batch_size)
         with torch.inference_mode():
-            self.static_lens = torch.zeros((batch_size,), dtype=torch.long, device=self.device)
-            self.metadata.cu_seqlens.zero_()
-            side = torch.cuda.Stream(device=self.device)
-            side.wait_stream(torch.cuda.current_stream(self.device))
-            with torch.cuda.stream(side):
-                for _ in range(max(1, warmup_iters)):
-                    self._forward()
-            torch.cuda.current_stream(self.device).wait_stream(side)
-            torch.cuda.synchronize(self.device)
-            self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph, pool=pool):
-                self.static_hidden = self._forward()
-        self.lens = self.static_lens
-        self.warmup(min(batch_size, kv_cache.n_slots - 1, token_count))
+            self.step = StepGraph(self._step, pool=pool, warmup=warmup_iters, device=self.device)
 
-    def _pad(self, slot_ids: list[int]) -> list[int]:
-        return pad_slot_ids(slot_ids, self.batch_size, self.kv_cache.unused_idx)
-
-    def _write_batch(self, slots: torch.Tensor, cu_seqlens: torch.Tensor, lens: torch.Tensor) -> None:
-        self.metadata.write_slot_ids(slots)
-        self.metadata.write_cu_seqlens(cu_seqlens)
-        self.static_lens.copy_(lens)
-
-    def replay(self) -> torch.Tensor:
-        self.graph.replay()
-        return self.static_hidden
+    def run(self) -> torch.Tensor:
+        return self.step.replay()
 
 
 class PiecewiseMixedModule(MixedModule):
-    """The stack compiled through the piecewise backend (see the module docstring).
+    """The decoder stack compiled through the piecewise backend.
 
-    ``buffer`` (1, >= token_count, H_q, D) receives the attention outputs; it can
-    be shared by the modules of every token bucket, as in the reference.
+    ``buffer`` (1, >= token_count, H_q, D) receives the attention outputs; the
+    modules of several token buckets may share it.  ``backend`` exposes how
+    many graphs it compiled and how many captured pieces it replayed.
     """
 
-    def __init__(self, model, kv_cache, token_count: int, buffer: torch.Tensor, pool=None):
-        super().__init__(model, kv_cache, token_count)
-        self.compiled = torch.compile(self._forward,
-                                      backend=get_piecewise_backend(buffer[:, :token_count], pool),
-                                      fullgraph=True, dynamic=False)
-        self.warmup(min(kv_cache.n_slots - 1, token_count))
-        self.warmup(1)
+    # Each bucket's module compiles the same ``_forward`` code once; the
+    # compiles all happen in the constructors (fixed shapes), under this limit.
+    RECOMPILE_LIMIT = 64
 
-    def _write_batch(self, slots: torch.Tensor, cu_seqlens: torch.Tensor, lens: torch.Tensor) -> None:
-        if len(slots) > 1:
-            torch._dynamo.mark_dynamic(slots, 0)
-            torch._dynamo.mark_dynamic(cu_seqlens, 0)
-        super()._write_batch(slots, cu_seqlens, lens)
+    def __init__(self, model, kv_cache, token_count: int, buffer: torch.Tensor, pool=None,
+                 batch_size: int | None = None):
+        super().__init__(model, kv_cache, token_count, batch_size=batch_size)
+        self.backend = get_piecewise_backend(buffer[:, :token_count], pool)
+        self.compiled = torch.compile(self._forward, backend=self.backend, fullgraph=True,
+                                      dynamic=False)
+        with self._compile_limits(), torch.inference_mode():
+            self._prepare()  # the all-padding inputs: slot 0 and page 0 only
+            self.compiled()
 
-    def replay(self) -> torch.Tensor:
-        return self.compiled()
+    @classmethod
+    def _compile_limits(cls):
+        dynamo = torch._dynamo.config
+        limits = {"recompile_limit": max(dynamo.recompile_limit, cls.RECOMPILE_LIMIT)}
+        if hasattr(dynamo, "accumulated_recompile_limit"):
+            limits["accumulated_recompile_limit"] = max(dynamo.accumulated_recompile_limit,
+                                                        cls.RECOMPILE_LIMIT)
+        return dynamo.patch(**limits) if hasattr(dynamo, "patch") else contextlib.nullcontext()
+
+    def _step(self) -> torch.Tensor:
+        self._prepare()
+        hidden = self.compiled()
+        self._advance()
+        return self._logits(hidden)

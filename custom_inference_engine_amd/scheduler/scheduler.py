@@ -120,10 +120,11 @@ def token_buckets(token_budget: int, min_bucket: int = 16, full_threshold: int =
 class ModuleExecutor:
     """Steps on the GPU through the step modules.
 
-    Every graph is captured here, before any request runs (a module's warm-up
-    writes through the slots it covers and then resets them): one
-    ``DecodeModule`` per batch bucket and, with ``graph_mixed``, one
-    ``FullMixedModule`` per token bucket at the largest batch bucket.
+    Every graph is captured here, before any request runs (the captures'
+    warm-ups touch only the reserved slot 0 and page 0): one ``DecodeModule``
+    per batch bucket and, with ``graph_mixed``, one ``FullMixedModule`` per
+    token bucket at the largest batch bucket (padded sequences cost nothing,
+    so one graph serves every batch size).
     Without it, mixed steps run eagerly (``MixedModule`` of the token bucket,
     made on first use).  With ``piecewise_above`` set, the token buckets above
     it use ``PiecewiseMixedModule`` instead, sharing one attention-output
@@ -148,16 +149,14 @@ class ModuleExecutor:
         self.mixed_modules = {}
         piecewise = [t for t in self.token_counts if piecewise_above is not None and t > piecewise_above]
         if graph_mixed and piecewise:
-            # two compiles per bucket (batch 1 and a dynamic batch), on one code object
-            torch._dynamo.config.recompile_limit = max(torch._dynamo.config.recompile_limit,
-                                                       2 * len(piecewise))
             self.buffer = torch.zeros((1, max(piecewise), kv_cache.num_q_heads, kv_cache.head_dim),
                                       dtype=kv_cache.dtype, device=kv_cache.device)
         if graph_mixed:
             for t in sorted(self.token_counts, reverse=True):
                 if t in piecewise:
                     self.mixed_modules[t] = PiecewiseMixedModule(model, kv_cache, token_count=t,
-                                                                 buffer=self.buffer, pool=self.pool)
+                                                                 buffer=self.buffer, pool=self.pool,
+                                                                 batch_size=self.max_batch)
                 else:
                     self.mixed_modules[t] = FullMixedModule(model, kv_cache, batch_size=self.max_batch,
                                                             token_count=t, pool=self.pool)
@@ -170,7 +169,8 @@ class ModuleExecutor:
 
         bucket = _smallest_fit(self.token_counts, n_tokens)
         if bucket not in self.mixed_modules:
-            self.mixed_modules[bucket] = MixedModule(self.model, self.kv_cache, token_count=bucket)
+            self.mixed_modules[bucket] = MixedModule(self.model, self.kv_cache, token_count=bucket,
+                                                     batch_size=self.max_batch)
         return self.mixed_modules[bucket]
 
     def decode(self, slot_ids: list[int]) -> list[int]:

@@ -1,4 +1,4 @@
-"""hipGraph capture (torch.cuda.CUDAGraph) of the decode and mixed steps.
+"""hipGraph capture (``graphs.StepGraph``) of the decode and mixed steps.
 
 Every replay is compared bit for bit with the same step run eagerly on a
 separate copy of the state, with eager work and synchronisations between
@@ -8,6 +8,7 @@ import pytest
 import torch
 
 from custom_inference_engine_amd import decode_gqa_attention, kv_append_decode, kv_append_tokens, mixed_gqa_attention
+from custom_inference_engine_amd.graphs import StepGraph
 from oracle import inputs
 from tests.conftest import assert_attn_close
 from tests.gpu_helpers import DEV, bits, note
@@ -35,6 +36,12 @@ class DecodeState:
         self.lens[self.slot_ids] += 1
         return o
 
+    def restore(self, case):
+        c = case.to(DEV)
+        self.kp.copy_(c.k_pool)
+        self.vp.copy_(c.v_pool)
+        self.lens.copy_(c.lens_pool)
+
     def load_inputs(self, gen):
         for t in (self.q, self.k_new, self.v_new):
             t.copy_((torch.randn(t.shape, generator=gen) * 0.5).half())
@@ -47,18 +54,10 @@ def test_decode_step_graph_replays_match_eager(native_lib):
     note("graph decode capture")
     graph_state, eager_state = DecodeState(case), DecodeState(case)
 
-    # warm up on a side stream with a throwaway copy, as the reference's DecodeModule does
-    warm = DecodeState(case)
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        warm.step()
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        static_out = graph_state.step()
+    # the capture's warm-up ran one eager step on graph_state: put it back
+    g = StepGraph(graph_state.step)
+    static_out = g.output
+    graph_state.restore(case)
     torch.cuda.synchronize()
 
     gen_g, gen_e = torch.Generator().manual_seed(5), torch.Generator().manual_seed(5)
@@ -97,14 +96,10 @@ def test_mixed_step_graph_replays_match_eager(native_lib):
                                    c.block_table)
 
     gs, es = make(), make()
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        step(make())
-    torch.cuda.current_stream().wait_stream(side)
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        static_out = step(gs)
+    g = StepGraph(lambda: step(gs))
+    static_out = g.output
+    gs["kp"].copy_(c.k_pool)  # the capture's warm-up appended once
+    gs["vp"].copy_(c.v_pool)
     torch.cuda.synchronize()
     gen_g, gen_e = torch.Generator().manual_seed(7), torch.Generator().manual_seed(7)
     T = case.T

@@ -68,7 +68,7 @@ def test_qwen2_model_mixed_prefill_then_graph_decode(native_lib):
     for step in range(3):
         note(f"model graph decode {step}")
         nxt = dec.forward(slots)
-        logits = dec.static_logits[:3].clone()
+        logits = dec.logits[:3].clone()
         for i in range(3):
             want = _ref_logits(ref, seqs[i])
             rel = _rel(logits[i], want)
@@ -111,9 +111,9 @@ def test_full_mixed_module_graph_matches_eager(native_lib):
 
 def test_piecewise_mixed_module_matches_eager(native_lib):
     """Steps through PiecewiseMixedModule (hipGraph pieces between eager varlen
-    attention calls, batch dimension dynamic) equal the eager module's: a prefill
-    of three prompts, decode rows for them, then batches of one and two sequences
-    (the batch-1 compile, then the dynamic one again)."""
+    attention calls) equal the eager module's: a prefill of three prompts, decode
+    rows for them, then batches of one and two sequences, all through the one
+    compile of the bucket."""
     from custom_inference_engine_amd.scheduler import PiecewiseMixedModule
 
     cfg, ref = _model()
@@ -145,6 +145,11 @@ def test_piecewise_mixed_module_matches_eager(native_lib):
         steps.append(mod.forward([[steps[-2][0]], [steps[-2][2], 3]], [1, 3]))
         logits.append(mod.last_logits.float().cpu())
         torch.cuda.synchronize()
+        if piecewise:
+            # one compile (fixed shapes), and every step replayed its recorded pieces
+            # (3 per step for 2 layers) instead of falling back to eager
+            assert mod.backend.compiles == 1
+            assert mod.backend.piece_replays >= 4 * 3
         results.append((steps, logits, kv.lens.cpu(), torch.stack(kv.keys).cpu(), torch.stack(kv.values).cpu()))
     (sa, la, lens_a, k_a, v_a), (sb, lb, lens_b, k_b, v_b) = results
     assert sa == sb

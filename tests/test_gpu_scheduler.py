@@ -64,3 +64,47 @@ def test_scheduler_serves_prompts_with_preemption(native_lib, piecewise):
                 f"request {i} token {j}: {tok} is {margin:.4f} below the best logit"
     # all slots and pages released; the pool forgot every sequence
     assert kv.lens.eq(0).all() and kv.block_table.eq(0).all()
+
+
+def test_scheduler_piecewise_buckets_stay_compiled(native_lib):
+    """With a 224-token budget the buckets above 128 (160, 192, 224) run through
+    PiecewiseMixedModule; several of them serve steps, and each compiled exactly
+    once and replayed its recorded pieces on every step it served (no eager
+    fallback after the constructors' compiles)."""
+    torch._dynamo.reset()
+    cfg = Qwen2Config(hidden_size=896, num_attention_heads=14, num_key_value_heads=2,
+                      intermediate_size=1024, num_hidden_layers=2, vocab_size=512,
+                      max_position_embeddings=4096, rope_theta=1e6, rms_norm_eps=1e-6,
+                      tie_word_embeddings=True)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    ref = Qwen2ForCausalLM(cfg).float().eval()
+    ours = copy.deepcopy(ref).half().to(DEV)
+    use_triton_attention(ours)
+    kv = KVStorage(cfg, max_cache_len=1024, page_size=16, n_slots=4, device=DEV, dtype=torch.float16)
+    note("scheduler: piecewise buckets")
+    sched = Scheduler(ours, kv, eos_token_ids={cfg.vocab_size}, max_new_tokens=4, token_budget=224,
+                      piecewise_mixed=True)
+    g = torch.Generator().manual_seed(12)
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist()
+               for n in (150, 20, 10, 140, 60, 20)]  # mixed steps of 180 and 220 tokens
+    with torch.inference_mode():
+        results = sched.generate(prompts)
+    torch.cuda.synchronize()
+    served = {t: n for t, n in sched.stats.mixed_steps.items() if t > 128}
+    assert len(served) >= 2, sched.stats.mixed_steps
+    for t, n in served.items():
+        mod = sched.executor.mixed_modules[t]
+        assert type(mod) is PiecewiseMixedModule
+        assert mod.backend.compiles == 1, (t, mod.backend.compiles)
+        # warm-up plus n steps, each replaying the 3 recorded pieces of a 2-layer stack
+        assert mod.backend.piece_replays == 3 * (n + 1), (t, n, mod.backend.piece_replays)
+    for p, r in zip(prompts, results):
+        assert len(r.new_tokens) == 4
+        seq = p + r.new_tokens
+        with torch.no_grad():
+            logits = ref(input_ids=torch.tensor([seq[:-1]]), use_cache=False).logits[0]
+        for j, tok in enumerate(r.new_tokens):
+            row = logits[len(p) - 1 + j]
+            assert float(row.max() - row[tok]) <= 2e-2 * float(row.max() - row.min())
+    assert kv.lens.eq(0).all() and kv.block_table.eq(0).all()

@@ -5,8 +5,8 @@ kernel runs: the recording backend stops before execution).
 The cut must leave every ``inference::gqa_mixed_attention`` call in an
 odd-numbered piece of its own, together with the gather of its ``kv_lens``,
 and nothing that reads the batch's per-sequence tensors (``slot_ids``,
-``cu_seqlens``, the batch size) in the even-numbered pieces, which are
-replayed from hipGraphs captured once for every batch size.
+``cu_seqlens``) in the even-numbered pieces, which are replayed from
+hipGraphs.
 """
 import re
 
@@ -48,9 +48,7 @@ def _traced_step(n_layers: int, chunks):
     torch._dynamo.reset()
     with torch.inference_mode():
         mod.upload([[1] * n for n in chunks], slots)
-        if len(slots) > 1:
-            torch._dynamo.mark_dynamic(mod.metadata.slot_ids, 0)
-            torch._dynamo.mark_dynamic(mod.metadata.cu_seqlens, 0)
+        mod._prepare()
         f = torch.compile(mod._forward, backend=backend, fullgraph=True, dynamic=False)
         with pytest.raises(_Traced):
             f()
