@@ -54,6 +54,13 @@ _SIGNATURES = {
          _c_i64p, _c_i64p, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
+    "cie_paged_decode_noalloc_limit": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "cie_paged_decode_append_noalloc": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64p,
+         _c_i64p, _c_i64p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
     "cie_paged_decode_qkv_rope": (
         ctypes.c_int,
         [_c_ptr, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64p, _c_i64p, _c_i64p,

@@ -11,6 +11,8 @@ extern "C" const char* cie_status_string(int status) {
       return "invalid argument (sizes, strides, alignment or null pointer)";
     case CIE_EUNSUPPORTED:
       return "unsupported shape for the gfx950 kernels";
+    case CIE_ESCRATCH:
+      return "problem larger than the allocation-free entry point's static scratch";
     default:
       break;
   }

@@ -31,6 +31,8 @@
 // arrival counter (arrive_last) — merges the splits with log-sum-exp as
 // kernels/decode_attention.py:243-264 does, writes o and resets the counter
 // to zero for the next call.
+#include <mutex>
+
 #include "attn_engine.h"
 
 // Build-time tuning (defaults are the shipped configuration):
@@ -804,4 +806,98 @@ extern "C" int cie_paged_decode_qkv_rope(
   return decode_entry<true, true>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages,
                                   pool_page_stride, pool_head_stride, bt_stride, bt_width,
                                   n_slots, n_splits, err, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of cie_paged_decode_append: the split partials and
+// arrival counters live in this file-scope device array instead of caller
+// buffers.  Each GPU holds its own copy for the life of the process; host
+// code reaches it only through the address hipGetSymbolAddress returns for
+// the current device (the array's name is a host-side stand-in, not a device
+// address).
+namespace cie {
+
+constexpr int64_t kScratchPartialBytes = int64_t(4) << 20;  // split partials
+constexpr int64_t kScratchCounterWords = 16384;             // 2 * B * H_kv arrival + stale words
+constexpr int64_t kScratchBytes = kScratchPartialBytes + kScratchCounterWords * 4;
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ void zero_words_kernel(int32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+struct ScratchSlot {
+  char* ptr = nullptr;
+  bool zeroed = false;
+};
+
+// The current device's scratch address; its counters are zeroed by a fill
+// kernel on `stream` the first time (a kernel, not a memset, so a first call
+// under graph capture records a kernel node).  Returns a CIE_* / hipError_t.
+static int device_scratch(hipStream_t stream, char** out) {
+  constexpr int kMaxDevices = 64;
+  static ScratchSlot slots[kMaxDevices];
+  static std::mutex mu;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return CIE_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(mu);
+  ScratchSlot& s = slots[dev];
+  if (s.ptr == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    s.ptr = static_cast<char*>(ptr);
+  }
+  if (!s.zeroed) {
+    hipLaunchKernelGGL(zero_words_kernel, dim3(16), dim3(256), 0, stream,
+                       reinterpret_cast<int32_t*>(s.ptr + kScratchPartialBytes), kScratchCounterWords);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    s.zeroed = true;
+  }
+  *out = s.ptr;
+  return CIE_OK;
+}
+
+}  // namespace cie
+
+extern "C" int64_t cie_paged_decode_noalloc_limit(int64_t H_q, int64_t D, int64_t n_splits) {
+  // largest batch whose partials and counters fit the static scratch (H_kv >= 1)
+  if (H_q <= 0 || D <= 0 || n_splits <= 0) return -1;
+  int64_t lo = 0, hi = kScratchCounterWords / 2;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (n_splits == 1 || part_layout(mid, H_q, D, n_splits).total <= kScratchPartialBytes)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+extern "C" int cie_paged_decode_append_noalloc(
+    void* o, const void* q, void* k_pool, void* v_pool, const void* k_new, const void* v_new,
+    int64_t k_tok_stride, int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+    const int64_t* lens, const int64_t* slot_ids, const int64_t* block_table, int64_t B,
+    int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size, int64_t n_pages,
+    int64_t pool_page_stride, int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
+    int64_t n_slots, int64_t n_splits, int32_t* err, void* stream) {
+  if (B < 0 || H_q <= 0 || H_kv <= 0 || D <= 0 || n_splits <= 0) return CIE_EINVAL;
+  if (B == 0) return CIE_OK;
+  if (2 * B * H_kv > kScratchCounterWords ||
+      (n_splits > 1 && part_layout(B, H_q, D, n_splits).total > kScratchPartialBytes))
+    return CIE_ESCRATCH;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = nullptr;
+  const int rc = device_scratch(s, &ws);
+  if (rc != CIE_OK) return rc;
+  return cie_paged_decode_append(o, q, k_pool, v_pool, k_new, v_new, k_tok_stride, k_head_stride,
+                                 v_tok_stride, v_head_stride, lens, slot_ids, block_table, ws,
+                                 reinterpret_cast<int32_t*>(ws + kScratchPartialBytes), B, H_q,
+                                 H_kv, D, page_size, n_pages, pool_page_stride, pool_head_stride,
+                                 bt_stride, bt_width, n_slots, n_splits, err, stream);
 }

@@ -35,6 +35,8 @@ extern "C" {
 #define CIE_OK 0
 #define CIE_EINVAL (-1)      /* inconsistent sizes / strides / null pointer      */
 #define CIE_EUNSUPPORTED (-2) /* shape outside what the kernels are built for   */
+#define CIE_ESCRATCH (-3)     /* problem larger than the static scratch of an
+                                 allocation-free entry point                     */
 
 #define CIE_ERRBIT_PAGE 1     /* page id outside [0, n_pages)                    */
 #define CIE_ERRBIT_LEN 2      /* length beyond the block-table row capacity      */
@@ -148,6 +150,35 @@ int cie_paged_decode_append(void* o, const void* q, void* k_pool, void* v_pool,
                             int64_t bt_stride, int64_t bt_width,
                             int64_t n_slots, int64_t n_splits, int32_t* err,
                             void* stream);
+
+/*
+ * Allocation-free form of cie_paged_decode_append.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * hipGraph stream capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and result as cie_paged_decode_append without
+ * `partials` / `counters`: those live in a static device array of this
+ * library (4 MiB of split partials plus 16,384 counter words, one copy per
+ * GPU, held until the process ends).  The counters are zeroed by a fill
+ * kernel on `stream` at the first call on a device and left zero by every
+ * completed call.  A problem whose partials (cie_paged_decode_partials_bytes)
+ * exceed 4 MiB or with 2 * B * H_kv > 16384 returns CIE_ESCRATCH and launches
+ * nothing; cie_paged_decode_noalloc_limit(H_q, D, n_splits) gives the largest
+ * B that fits.  Every call on one GPU shares the array: calls that can
+ * overlap in time on one GPU (different streams) race and must not be made.
+ */
+int64_t cie_paged_decode_noalloc_limit(int64_t H_q, int64_t D, int64_t n_splits);
+int cie_paged_decode_append_noalloc(void* o, const void* q, void* k_pool, void* v_pool,
+                                    const void* k_new, const void* v_new,
+                                    int64_t k_tok_stride, int64_t k_head_stride,
+                                    int64_t v_tok_stride, int64_t v_head_stride,
+                                    const int64_t* lens, const int64_t* slot_ids,
+                                    const int64_t* block_table,
+                                    int64_t B, int64_t H_q, int64_t H_kv, int64_t D,
+                                    int64_t page_size, int64_t n_pages,
+                                    int64_t pool_page_stride, int64_t pool_head_stride,
+                                    int64_t bt_stride, int64_t bt_width,
+                                    int64_t n_slots, int64_t n_splits, int32_t* err,
+                                    void* stream);
 
 /*
  * Decode step from the fused QKV projection, RoPE and KV append fused in, one
