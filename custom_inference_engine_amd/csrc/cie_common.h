@@ -185,6 +185,7 @@ __device__ __forceinline__ bool arrive_last(int32_t* arrival, int64_t n_words, i
   return *sm_flag != 0;
 }
 
+
 // Uniform (wave-invariant) value hint: lets the compiler keep it in an SGPR.
 __device__ __forceinline__ int uniform(int x) {
   return __builtin_amdgcn_readfirstlane(x);

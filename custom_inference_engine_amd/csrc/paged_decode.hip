@@ -194,24 +194,31 @@ __device__ __forceinline__ float partial_load(const float* ptr) { return agent_l
 constexpr int kMaxSplits = 64;
 
 template <int D, int NTHREADS>
-__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g);
+__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g, int n_states,
+                                             int tid);
 
-// Profiling builds only (-DCIE_DECODE_TRACE): wave 0 of every workgroup
-// stamps phase boundaries (s_memrealtime) into a trace buffer of its own,
-// named by cie_decode_trace_buffer() (exported by such builds alone), 24
-// words per workgroup.  A stamp waits for nothing but its own clock read.
+// Profiling builds only (-DCIE_DECODE_TRACE): phase boundaries
+// (s_memrealtime) are stamped into LDS — LDS writes do not count in vmcnt, so
+// the stamps do not lengthen the waits on the K/V loads — and each workgroup
+// copies its 24 stamps to the buffer named by cie_decode_trace_buffer()
+// (exported by such builds alone) when it exits.
 #ifdef CIE_DECODE_TRACE
 constexpr int kTraceSlots = 24;
 __device__ uint64_t* g_decode_trace;
-#define DECODE_TRACE_LANE0(k, v)                                                               \
-  do {                                                                                         \
-    if ((threadIdx.x & (kWave - 1)) == 0 && g_decode_trace != nullptr) {                     \
-      g_decode_trace[((int64_t)(b * p.H_kv + g) * p.n_splits + split) * kTraceSlots + (k)] = (v); \
-    }                                                                                          \
+#define DECODE_TRACE_LANE0(k, v)                              \
+  do {                                                        \
+    if ((threadIdx.x & (kWave - 1)) == 0) sm_trace[(k)] = (v); \
   } while (0)
 #define DECODE_TRACE(k, v)                  \
   do {                                      \
-    if (threadIdx.x < kWave) DECODE_TRACE_LANE0(k, v); \
+    if (threadIdx.x == 0) sm_trace[(k)] = (v); \
+  } while (0)
+#define DECODE_TRACE_DUMP()                                                                          \
+  do {                                                                                               \
+    __syncthreads();                                                                                 \
+    if (threadIdx.x < kTraceSlots && g_decode_trace != nullptr)                                      \
+      g_decode_trace[((int64_t)(b * p.H_kv + g) * p.n_splits + split) * kTraceSlots + threadIdx.x] = \
+          sm_trace[threadIdx.x];                                                                     \
   } while (0)
 #else
 #define DECODE_TRACE_LANE0(k, v) \
@@ -219,6 +226,9 @@ __device__ uint64_t* g_decode_trace;
   } while (0)
 #define DECODE_TRACE(k, v) \
   do {                     \
+  } while (0)
+#define DECODE_TRACE_DUMP() \
+  do {                      \
   } while (0)
 #endif
 
@@ -232,6 +242,11 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   // rows padded to keep 16-byte alignment for the vector reads of the fold
   __shared__ f32x4 sm_acc[WAVES][16][D / 4 + 1];
   __shared__ int sm_last;
+#ifdef CIE_DECODE_TRACE
+  __shared__ uint64_t sm_trace[kTraceSlots];
+  if (threadIdx.x < kTraceSlots) sm_trace[threadIdx.x] = 0;
+  __syncthreads();
+#endif
 
   const int split = blockIdx.x;
   const int g = blockIdx.y;
@@ -273,7 +288,9 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
     }
     return (int)page;
   };
-  constexpr int kSpecTiles = 16;
+  // One page id per lane: a wave of up to 64 tiles (its odd last tile
+  // included) never waits on another block-table load before streaming.
+  constexpr int kSpecTiles = kWave;
   // Every load of the start goes out before any check: a check's error store
   // (set_err) may alias later loads as far as the compiler knows, so a check
   // placed between two loads makes the second wait for the first's data.
@@ -301,15 +318,6 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
     }
   }
 
-  int pages = 0;
-  if (lane < kSpecTiles && t_spec < row_tiles) {
-    int64_t page = page_spec;
-    if (page < 0 || page >= p.n_pages) {
-      set_err(p.err, CIE_ERRBIT_PAGE);
-      page = 0;
-    }
-    pages = (int)page;
-  }
   int L, pos = -1;
   {
     const int64_t cap = (int64_t)row_tiles * 16;
@@ -333,6 +341,17 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
   }
   const int n_tiles = (L + 15) >> 4;
   const int n_mine = n_tiles > gw ? (n_tiles - gw + TW - 1) / TW : 0;
+  // Speculatively fetched page ids of tiles past the sequence are never used
+  // (and never reported: the row may hold anything there).
+  int pages = 0;
+  if (lane < kSpecTiles && t_spec < n_tiles) {
+    int64_t page = page_spec;
+    if (page < 0 || page >= p.n_pages) {
+      set_err(p.err, CIE_ERRBIT_PAGE);
+      page = 0;
+    }
+    pages = (int)page;
+  }
 
   const PagedSrc src{p.k_pool,  p.v_pool,  bt_row, (int64_t)g * p.pool_head_stride,
                      p.pool_page_stride, p.n_pages, p.page_size, p.err};
@@ -450,6 +469,7 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
           }
           attend_pair<D, 1>(st, cur, QRegs<D, 1>{qop}, ka, kb, lim, L, p.scale_log2, grp);
         }
+        if (c0 == 0 && j == 0) DECODE_TRACE_LANE0(20 + wave, __builtin_amdgcn_s_memrealtime());
         if (odd && c0 == 0 && j == 0) attend_odd();
       }
     }
@@ -517,16 +537,23 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
     }
   }
   DECODE_TRACE(9, __builtin_amdgcn_s_memrealtime());
-  if (S == 1) return;
+  if (S == 1) {
+    DECODE_TRACE_DUMP();
+    return;
+  }
 
   // The last workgroup of this (sequence, kv head) to arrive merges the splits.
   int32_t* const arrival = p.counters + b * p.H_kv + g;
   const bool last = arrive_last(arrival, (int64_t)p.B * p.H_kv, S, &sm_last, p.err);
   DECODE_TRACE(10, __builtin_amdgcn_s_memrealtime());
-  if (!last) return;
-  merge_splits<D, WAVES * kWave>(p, b, g);
+  if (!last) {
+    DECODE_TRACE_DUMP();
+    return;
+  }
+  merge_splits<D, WAVES * kWave>(p, b, g, S, threadIdx.x);
   if (threadIdx.x == 0) counter_reset(arrival);
   DECODE_TRACE(4, __builtin_amdgcn_s_memrealtime());
+  DECODE_TRACE_DUMP();
 }
 
 // Combine the S partial states of every head of (b, g) into o.  A thread
@@ -538,13 +565,14 @@ __global__ __launch_bounds__(WAVES * kWave) void decode_kernel(DecodeParams p) {
 constexpr int kMergeGroup = 8;
 
 template <int D, int NTHREADS>
-__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g) {
+__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g, int n_states,
+                                             int tid) {
   constexpr int D4 = D / 4;
-  const int S = p.n_splits;
+  const int S = n_states;
   const int64_t row0 = ((int64_t)b * p.H_q + g * p.G) * S;
   const __amdgpu_buffer_rsrc_t racc =
       coherent_rsrc(p.part_acc + row0 * D, (uint32_t)(p.G * S * D * sizeof(float)));
-  for (int it = threadIdx.x; it < p.G * D4; it += NTHREADS) {
+  for (int it = tid; it < p.G * D4; it += NTHREADS) {
     const int h = it / D4;
     const int d4 = it - h * D4;
     const int r0 = h * S;  // partial row of (h, split 0) within (b, g)

@@ -195,3 +195,23 @@ def test_decode_stale_counter_is_flagged_and_cleared(native_lib):
     assert int(err.item()) == 0
     assert torch.count_nonzero(ctr) == 0
     assert_attn_close(o[0].float().cpu(), want, what="call after the stale one")
+
+
+def test_decode_ignores_block_table_entries_past_the_sequence(native_lib):
+    """The kernel fetches page ids ahead of knowing each sequence's length; entries of
+    a block-table row past the sequence's pages may hold anything (here: -7 and ids
+    beyond the pool) and must neither raise CIE_ERRBIT_PAGE nor change the result."""
+    case = inputs.make_case([30, 300, 1000, 5], seed=54)
+    note("decode garbage past the sequence")
+    bt = case.block_table.clone()
+    for b in range(case.B):
+        s = int(case.slot_ids[b])
+        used = -(-int(case.attended[b]) // 16)
+        bt[s, used:] = torch.where(torch.arange(bt.shape[1] - used) % 2 == 0, -7, bt.shape[1] + 100)
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    err = err_word()
+    o = decode_gqa_attention(c.q, kp, vp, c.attended, c.slot_ids, bt.to(DEV), num_programs=4, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert_attn_close(o[0].float().cpu(), oracle_decode(case), what="garbage past the sequence")
