@@ -60,6 +60,15 @@ def parse():
     ap.add_argument("--probe-sweep", action="store_true",
                     help="gather-probe rate by read volume and chunk size (the paged-read ceiling)")
     ap.add_argument("--repeats", type=int, default=5)
+    ap.add_argument("--kernels", action="store_true",
+                    help="per-launch times of the append kernels (decode B=32, token T=1052, fused "
+                         "QKV-split + RoPE T=1052) and of the rope-mode decode at config 2")
+    ap.add_argument("--trace-decode", action="store_true",
+                    help="phase trace of one config-2 call; needs a trace build of the library "
+                         "(python -m custom_inference_engine_amd._build -D CIE_DECODE_TRACE --out DIR, "
+                         "then CIE_PAGED_LIB=DIR/libcie_paged.so)")
+    ap.add_argument("--mixed-part", choices=("all", "prefill", "decode"), default="all",
+                    help="config 3: time only its prefill chunks or only its decode rows")
     return ap.parse_args()
 
 
@@ -198,6 +207,140 @@ def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chun
     return us, n * chunk
 
 
+def bench_kernels(args):
+    """Per-launch times (hipGraph replay of R launches over rotating inputs) of
+    the kernels the drop-in runs besides the headline call: the standalone KV
+    appends (decode mode at config 2's B = 32; token mode and the fused
+    QKV-split + RoPE + append at config 3's T = 1052) and the rope-mode decode
+    (QKV split + RoPE + append + split-KV decode in one launch) at config 2.
+    A one-element torch add is timed beside them: the floor of a launch that
+    loads and stores one value."""
+    import custom_inference_engine_amd as cie
+    from oracle import inputs
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev).manual_seed(3)
+
+    def rnd(*shape):
+        return (torch.randn(shape, generator=gen, device=dev) * 0.5).half()
+
+    def timed(fns):
+        # graphs of >= 128 launches: a replay of a few microsecond-scale kernels
+        # is shorter than the host's graph launch, which would then be timed
+        fns = fns * max(1, -(-128 // len(fns)))
+        return time_calls(fns, max(args.steps, 4 * len(fns)), args.warmup, True, args.repeats)
+
+    out = {}
+    one = torch.zeros(1, device=dev)
+    us, _ = timed([lambda: one.add_(1.0)])
+    out["floor_one_element_add"] = us
+    log(f"one-element add (launch floor): {us:.2f} us")
+
+    case2 = inputs.config2(seed=0)
+    c2 = case2.to(dev)
+    R = max(1, -(-MIN_ROTATION_BYTES // (2 * case2.k_pool.numel() * 2)))
+    pools = [(c2.k_pool.clone(), c2.v_pool.clone()) for _ in range(R)]
+    us, _ = timed([lambda kp=kp, vp=vp: cie.kv_append_decode(kp, vp, c2.k_new, c2.v_new, c2.slot_ids,
+                                                             c2.lens_pool, c2.block_table)
+                   for kp, vp in pools])
+    out["kv_append_decode_b32"] = us
+    log(f"kv_append_kernel<8,true> (decode append, B={case2.B}): {us:.2f} us")
+    qkvs = [rnd(1, case2.B, (14 + 4) * 64) for _ in range(R)]
+    cos, sin = rnd(1, case2.B, 64), rnd(1, case2.B, 64)
+    us, _ = time_calls([lambda i=i: cie.decode_qkv_rope_gqa_attention(qkvs[i], cos, sin, pools[i][0], pools[i][1],
+                                                                      c2.lens_pool, c2.slot_ids, c2.block_table,
+                                                                      num_heads=14)
+                        for i in range(R)], args.steps, args.warmup, True, args.repeats)  # ~17 us each
+    out["decode_rope_config2"] = us
+    log(f"decode_kernel<64,4,true,true> (rope mode, config 2): {us:.2f} us")
+    del pools
+
+    case3 = inputs.config3(seed=0)
+    c3 = case3.to(dev)
+    T = case3.T
+    pools = [(c3.k_pool.clone(), c3.v_pool.clone()) for _ in range(4)]
+    us, _ = timed([lambda kp=kp, vp=vp: cie.kv_append_tokens(kp, vp, c3.k_new, c3.v_new, c3.pages, c3.offsets)
+                   for kp, vp in pools])
+    out["kv_append_tokens_t1052"] = us
+    log(f"kv_append_kernel<8,false> (token append, T={T}): {us:.2f} us")
+    qkv3 = [rnd(1, T, (14 + 4) * 64) for _ in range(4)]
+    cos3, sin3 = rnd(1, T, 64), rnd(1, T, 64)
+    us, _ = timed([lambda i=i: cie.append_tokens_qkv_rope(qkv3[i], cos3, sin3, pools[i][0], pools[i][1],
+                                                          c3.pages, c3.offsets, num_heads=14)
+                   for i in range(4)])
+    out["qkv_rope_append_t1052"] = us
+    log(f"qkv_rope_append_kernel (QKV split + RoPE + append, T={T}): {us:.2f} us")
+    print(json.dumps({"metric": "per-launch us of the append kernels and the rope-mode decode",
+                      "unit": "us", "higher_is_better": False,
+                      **{k: round(v, 3) for k, v in out.items()}}), flush=True)
+
+
+def trace_decode(args):
+    """Phase trace of one config-2 call (append fused) after R warm calls.
+
+    A trace build stamps s_memrealtime (100 MHz) into LDS at phase boundaries
+    and each workgroup copies its stamps out as it exits; printed: per phase
+    the min / median / max over workgroups (µs from the first workgroup's
+    start), the loop end by XCD, and per split and wave the first step and
+    the loop end."""
+    import collections
+    import ctypes
+
+    import custom_inference_engine_amd as cie
+    from custom_inference_engine_amd import _native
+    from oracle import inputs
+
+    lib = _native.load()
+    if not hasattr(lib, "cie_decode_trace_buffer"):
+        raise SystemExit("--trace-decode needs a trace build (see --help)")
+    lib.cie_decode_trace_buffer.argtypes = [ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    case = inputs.config2(seed=0)
+    c = case.to(dev)
+    S = args.splits or cie.attn.core.default_decode_splits(case.B, 2, dev)
+    W, slots = 4, 24
+    R = max(1, -(-MIN_ROTATION_BYTES // (2 * case.k_pool.numel() * 2)))
+    pools = [(c.k_pool.clone(), c.v_pool.clone()) for _ in range(R)]
+    buf = torch.zeros(case.B * 2 * S * slots, dtype=torch.int64, device=dev)
+    if lib.cie_decode_trace_buffer(buf.data_ptr()) != 0:
+        raise SystemExit("cie_decode_trace_buffer failed")
+    for it in range(3 * R):
+        kp, vp = pools[it % R]
+        buf.zero_()
+        cie.decode_append_gqa_attention(c.q, kp, vp, c.k_new, c.v_new, c.lens_pool, c.slot_ids,
+                                        c.block_table, num_programs=S)
+    torch.cuda.synchronize()
+    lib.cie_decode_trace_buffer(None)
+    t = buf.view(-1, slots).cpu()
+    t0 = t[:, 0].min().item()
+
+    def us(v):
+        return (v - t0) / 100.0
+
+    phases = {0: "workgroup start", 1: "slot -> pages + length + Q known", 8: "fold barrier",
+              9: "partials issued", 10: "arrival atomic returned", 4: "merge end (last arriver)"}
+    for k, name in phases.items():
+        v = [us(x) for x in t[:, k].tolist() if x]
+        if v:
+            print(f"{name:34s} min {min(v):6.2f}  median {statistics.median(v):6.2f}  max {max(v):6.2f}")
+    ends = [us(max(t[r, 16:16 + W].tolist())) for r in range(t.shape[0])]
+    print(f"{'slowest wave of the workgroup ends':34s} min {min(ends):6.2f}  median "
+          f"{statistics.median(ends):6.2f}  max {max(ends):6.2f}")
+    by_xcd = collections.defaultdict(list)
+    for r in range(t.shape[0]):
+        by_xcd[int(t[r, 6].item()) & 0xF].append(ends[r])
+    print("loop end by XCD (median/max): " + "  ".join(
+        f"{x}:{statistics.median(v):.2f}/{max(v):.2f}" for x, v in sorted(by_xcd.items())))
+    for sp in range(S):
+        rows = [r for r in range(t.shape[0]) if r % S == sp]
+        for w in range(W):
+            first = [us(t[r, 20 + w].item()) for r in rows if t[r, 20 + w].item()]
+            end = [us(t[r, 16 + w].item()) for r in rows]
+            print(f"split {sp} wave {w}: first step done {statistics.median(first):6.2f}  "
+                  f"loop end median {statistics.median(end):6.2f} max {max(end):6.2f}")
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -249,6 +392,10 @@ def main():
         return copy_calibration(args)
     if args.probe_sweep:
         return probe_sweep(args)
+    if args.kernels:
+        return bench_kernels(args)
+    if args.trace_decode:
+        return trace_decode(args)
 
     import custom_inference_engine_amd as cie
     from custom_inference_engine_amd import _native
@@ -418,8 +565,16 @@ def main():
 
 
 def bench_mixed(args, cie, inputs, ref, dev):
-    """Config 3 (mixed chunked prefill + decode): us/call of append + mixed attention."""
+    """Config 3 (mixed chunked prefill + decode): us/call of append + mixed attention.
+
+    ``--mixed-part prefill`` / ``decode`` time the config's 4 prefill chunks or
+    its 28 decode rows alone (the same draws), e.g. to read the MFMA counters
+    of the prefill tiles without the decode rows."""
     case = inputs.config3(seed=0)
+    if args.mixed_part != "all":
+        prior, new = case.kv_lens.tolist(), case.new_lens.tolist()
+        keep = [i for i, n in enumerate(new) if (n > 1) == (args.mixed_part == "prefill")]
+        case = inputs.make_case([prior[i] for i in keep], [new[i] for i in keep], seed=0)
     c = case.to(dev)
     pool_bytes = 2 * case.k_pool.numel() * 2
     R = max(1, -(-MIN_ROTATION_BYTES // pool_bytes))
@@ -463,20 +618,24 @@ def bench_mixed(args, cie, inputs, ref, dev):
         keys = sum(cc + i + 1 for i in range(L))
         flops += 4 * 14 * 64 * keys
     print(json.dumps({
-        "metric": "mixed varlen chunked prefill + decode us/call (config 3)",
+        "metric": "mixed varlen chunked prefill + decode us/call (config 3)" if args.mixed_part == "all"
+        else f"mixed varlen attention us/call (config 3, its {args.mixed_part} part only)",
         "value": round(us, 3), "unit": "us/call", "higher_is_better": False, "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6),
         "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
         "achieved_TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
         "us_mixed_kernel": round(us_mix, 3),
         "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
-        "config": {"workload": "config 3 mixed: 4x256-row prefill chunks + 28 decode rows", "T": case.T,
+        "config": {"workload": {"all": "config 3 mixed: 4x256-row prefill chunks + 28 decode rows",
+                                "prefill": "config 3's 4x256-row prefill chunks alone",
+                                "decode": "config 3's 28 decode rows alone"}[args.mixed_part], "T": case.T,
                    "algorithmic_bytes": nbytes, "flops": flops, "layer_rotation": R},
         "roofline": {"bound": "mfma", "kernel": "mixed_attention_kernel<64>",
                      "achieved": round(flops / (us_mix * 1e-6) / 1e12, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / (us_mix * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
                      "hbm_frac": round((nbytes - app) / (us_mix * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-                     "traffic": TRAFFIC_BYTES[3][0], "traffic_source": TRAFFIC_BYTES[3][1]},
+                     "traffic": TRAFFIC_BYTES[3][0] if args.mixed_part == "all" else None,
+                     "traffic_source": TRAFFIC_BYTES[3][1] if args.mixed_part == "all" else None},
         "parity_max_abs_err": err,
     }), flush=True)
 

@@ -50,20 +50,32 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   const int h = (int)((gid / chunks) % p.H_kv);
   const int64_t row = gid / ((int64_t)chunks * p.H_kv);
 
+  // Every load that does not depend on another goes out first: the new rows
+  // (always in bounds) and the row's index (slot id, or page and offset), so
+  // the kernel's memory round trips are only the ones the index chain forces
+  // (decode: slot -> lens[slot] -> block_table[slot, pos / page_size]; token
+  // mode: none after the first).  The checks come after the loads: an error
+  // store between two loads would make the second wait for the first.
+  const vec_t kv = *reinterpret_cast<const vec_t*>(p.k_new + row * p.k_tok_stride +
+                                                   h * p.k_head_stride + c * VEC);
+  const vec_t vv = *reinterpret_cast<const vec_t*>(p.v_new + row * p.v_tok_stride +
+                                                   h * p.v_head_stride + c * VEC);
   int64_t page, off;
   if constexpr (kDecode) {
     const int64_t slot = p.slot_ids[row];
-    if (slot < 0 || slot >= p.n_slots) {
+    const bool slot_ok = slot >= 0 && slot < p.n_slots;
+    const int64_t pos = p.lens[slot_ok ? slot : 0];
+    const bool pos_ok = pos >= 0 && pos < p.bt_width * p.page_size;
+    page = p.block_table[(slot_ok ? slot : 0) * p.bt_stride + (pos_ok ? pos / p.page_size : 0)];
+    off = pos % p.page_size;
+    if (!slot_ok) {
       set_err(p.err, CIE_ERRBIT_PAGE);
       return;
     }
-    const int64_t pos = p.lens[slot];
-    if (pos < 0 || pos >= p.bt_width * p.page_size) {
+    if (!pos_ok) {
       set_err(p.err, CIE_ERRBIT_LEN);
       return;
     }
-    page = p.block_table[slot * p.bt_stride + pos / p.page_size];
-    off = pos % p.page_size;
   } else {
     page = p.pages[row];
     off = p.offsets[row];
@@ -76,13 +88,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
     set_err(p.err, CIE_ERRBIT_PAGE);
     return;
   }
-
-  const int64_t dst = page * p.pool_page_stride + h * p.pool_head_stride +
-                      off * p.D + (int64_t)c * VEC;
-  const vec_t kv = *reinterpret_cast<const vec_t*>(
-      p.k_new + row * p.k_tok_stride + h * p.k_head_stride + c * VEC);
-  const vec_t vv = *reinterpret_cast<const vec_t*>(
-      p.v_new + row * p.v_tok_stride + h * p.v_head_stride + c * VEC);
+  const int64_t dst = page * p.pool_page_stride + h * p.pool_head_stride + off * p.D + (int64_t)c * VEC;
   *reinterpret_cast<vec_t*>(p.k_pool + dst) = kv;
   *reinterpret_cast<vec_t*>(p.v_pool + dst) = vv;
 }
@@ -120,6 +126,9 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(QkvRopeParams p) {
   const int half = p.D / 2;
   const int d0 = 8 * c;
 
+  // All loads first (one memory round trip): the token's rotary rows, its
+  // q / k / v dims, and for kv heads the page and in-page offset.
+  const bool kv_head = h >= p.H_q;
   const f16* crow = p.cos + t * p.cs_stride;
   const f16* srow = p.sin + t * p.cs_stride;
   const f16x8 c_lo = *reinterpret_cast<const f16x8*>(crow + d0);
@@ -129,17 +138,23 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(QkvRopeParams p) {
   const f16* x = p.qkv + t * p.qkv_stride + (int64_t)h * p.D;
   f16x8 lo = *reinterpret_cast<const f16x8*>(x + d0);
   f16x8 hi = *reinterpret_cast<const f16x8*>(x + d0 + half);
+  f16x8 v_lo = {}, v_hi = {};
+  int64_t page = 0, off = 0;
+  if (kv_head) {
+    const f16* v = x + (int64_t)p.H_kv * p.D;  // v block: H_kv heads after k
+    v_lo = *reinterpret_cast<const f16x8*>(v + d0);
+    v_hi = *reinterpret_cast<const f16x8*>(v + d0 + half);
+    page = p.pages[t];
+    off = p.offsets[t];
+  }
   rope8(lo, hi, c_lo, c_hi, s_lo, s_hi);
 
-  if (h < p.H_q) {
+  if (!kv_head) {
     f16* dst = p.q_out + (t * p.H_q + h) * p.D;
     *reinterpret_cast<f16x8*>(dst + d0) = lo;
     *reinterpret_cast<f16x8*>(dst + d0 + half) = hi;
     return;
   }
-  const int hk = h - p.H_q;
-  const int64_t page = p.pages[t];
-  const int64_t off = p.offsets[t];
   if (off < 0 || off >= p.page_size) {
     set_err(p.err, CIE_ERRBIT_OFFSET);
     return;
@@ -148,13 +163,12 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(QkvRopeParams p) {
     set_err(p.err, CIE_ERRBIT_PAGE);
     return;
   }
+  const int hk = h - p.H_q;
   const int64_t row = page * p.pool_page_stride + hk * p.pool_head_stride + off * p.D;
   *reinterpret_cast<f16x8*>(p.k_pool + row + d0) = lo;
   *reinterpret_cast<f16x8*>(p.k_pool + row + d0 + half) = hi;
-  const f16* v = x + (int64_t)p.H_kv * p.D;  // v block: H_kv heads after k
-  *reinterpret_cast<f16x8*>(p.v_pool + row + d0) = *reinterpret_cast<const f16x8*>(v + d0);
-  *reinterpret_cast<f16x8*>(p.v_pool + row + d0 + half) =
-      *reinterpret_cast<const f16x8*>(v + d0 + half);
+  *reinterpret_cast<f16x8*>(p.v_pool + row + d0) = v_lo;
+  *reinterpret_cast<f16x8*>(p.v_pool + row + d0 + half) = v_hi;
 }
 
 static bool aligned16(const void* ptr) {
