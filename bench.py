@@ -67,6 +67,9 @@ def parse():
                     help="phase trace of one config-2 call; needs a trace build of the library "
                          "(python -m custom_inference_engine_amd._build -D CIE_DECODE_TRACE --out DIR, "
                          "then CIE_PAGED_LIB=DIR/libcie_paged.so)")
+    ap.add_argument("--trace-mixed", action="store_true",
+                    help="per-item phase trace of one config-3 mixed launch; needs a trace build "
+                         "(-D CIE_MIXED_TRACE, loaded through CIE_PAGED_LIB)")
     ap.add_argument("--mixed-part", choices=("all", "prefill", "decode"), default="all",
                     help="config 3: time only its prefill chunks or only its decode rows")
     return ap.parse_args()
@@ -341,6 +344,84 @@ def trace_decode(args):
                   f"loop end median {statistics.median(end):6.2f} max {max(end):6.2f}")
 
 
+def trace_mixed(args):
+    """Per-item phase trace of one config-3 mixed launch (``--mixed-part`` applies).
+
+    Each work item's stamps (µs from the first item's start): start, tile
+    lookup done, Q staged, key loop done, fold done, end (plus merge for the
+    last chunk of a split tile).  Printed: the span, the critical item, and
+    per item class (column tiles x chunked) the median phase durations."""
+    import ctypes
+
+    import custom_inference_engine_amd as cie
+    from custom_inference_engine_amd import _native
+    from oracle import inputs
+
+    lib = _native.load()
+    if not hasattr(lib, "cie_mixed_trace_buffer"):
+        raise SystemExit("--trace-mixed needs a trace build (see --help)")
+    lib.cie_mixed_trace_buffer.argtypes = [ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    case = inputs.config3(seed=0)
+    if args.mixed_part != "all":
+        prior, new = case.kv_lens.tolist(), case.new_lens.tolist()
+        keep = [i for i, n in enumerate(new) if (n > 1) == (args.mixed_part == "prefill")]
+        case = inputs.make_case([prior[i] for i in keep], [new[i] for i in keep], seed=0)
+    c = case.to(dev)
+    R = 8
+    pools = [(c.k_pool.clone(), c.v_pool.clone()) for _ in range(R)]
+    buf = torch.zeros(2 * 4096 * 16, dtype=torch.int64, device=dev)
+    if lib.cie_mixed_trace_buffer(buf.data_ptr()) != 0:
+        raise SystemExit("cie_mixed_trace_buffer failed")
+    for it in range(3 * R):
+        kp, vp = pools[it % R]
+        buf.zero_()
+        cie.mixed_gqa_attention(c.q, kp, vp, 256, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table)
+    torch.cuda.synchronize()
+    lib.cie_mixed_trace_buffer(None)
+    t = buf.view(2, 4096, 16).cpu()
+    valid = t[:, :, 0] != 0
+    t0 = t[:, :, 0][valid].min().item()
+
+    def us(x):
+        return (x - t0) / 100.0
+
+    items = []
+    for g in range(2):
+        for i in range(4096):
+            if not valid[g, i]:
+                continue
+            r = t[g, i].tolist()
+            info = r[5]
+            items.append(dict(g=g, item=i, start=us(r[0]), lookup=us(r[1]), q=us(r[9]), loop=us(r[8]),
+                              fold=us(r[2]), end=us(r[3]), merge=us(r[4]) if r[4] else None,
+                              nct=info // 1000000, nch=(info // 10000) % 100, ktiles=info % 10000,
+                              seq=r[7] // 1000, qt=r[7] % 1000))
+    span = max(x["end"] for x in items)
+    crit = max(items, key=lambda x: x["end"])
+    print(f"items {len(items)}, span {span:.2f} us; planning done (median over workgroups) "
+          f"{statistics.median(us(t[g, i, 6].item()) for g in range(2) for i in range(4096) if t[g, i, 6]):.2f} us")
+    print("critical item: " + ", ".join(f"{k} {v:.2f}" if isinstance(v, float) else f"{k} {v}"
+                                        for k, v in crit.items()))
+    print(f"{'class':18s} {'n':>4s} {'start':>6s} {'lookup':>7s} {'Q':>6s} {'loop':>7s} {'fold':>6s} "
+          f"{'end':>6s} {'end max':>8s}  (µs; start absolute, the rest after the item's start)")
+    for nct in (1, 2, 3, 4):
+        for chunked in (False, True):
+            sel = [x for x in items if x["nct"] == nct and (x["nch"] > 1) == chunked]
+            if not sel:
+                continue
+            med = lambda k: statistics.median(x[k] - x["start"] for x in sel)
+            print(f"{nct} col tile(s){' chunked' if chunked else '':8s} {len(sel):4d} "
+                  f"{statistics.median(x['start'] for x in sel):6.2f} {med('lookup'):7.2f} {med('q'):6.2f} "
+                  f"{med('loop'):7.2f} {med('fold'):6.2f} {med('end'):6.2f} "
+                  f"{max(x['end'] - x['start'] for x in sel):8.2f}")
+    late = sorted(items, key=lambda x: -x["end"])[:8]
+    print("latest items (seq, tile, col tiles, chunks, key tiles: start -> end):")
+    for x in late:
+        print(f"  seq {x['seq']} tile {x['qt']} ct {x['nct']} ch {x['nch']} kt {x['ktiles']}: "
+              f"{x['start']:.2f} -> {x['end']:.2f} (loop {x['loop'] - x['start']:.2f})")
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -396,6 +477,8 @@ def main():
         return bench_kernels(args)
     if args.trace_decode:
         return trace_decode(args)
+    if args.trace_mixed:
+        return trace_mixed(args)
 
     import custom_inference_engine_amd as cie
     from custom_inference_engine_amd import _native

@@ -216,20 +216,31 @@ __device__ __forceinline__ int column_off(const MixedParams& p, int g, int cc) {
 }
 
 // Profiling builds only (-DCIE_MIXED_TRACE): thread 0 stamps each work item's
-// phases (s_memrealtime) into a trace buffer of its own, named by
-// cie_mixed_trace_buffer() (exported by such builds alone), 16 words per
-// (kv head, item).
+// phases (s_memrealtime, 100 MHz) into LDS — LDS writes do not count in
+// vmcnt, so the stamps add no wait on the K/V loads — and copies the item's
+// 16 words to the buffer named by cie_mixed_trace_buffer() (exported by such
+// builds alone) when the item ends, at [kv head][item][16].
 #ifdef CIE_MIXED_TRACE
 __device__ uint64_t* g_mixed_trace;
-#define MIXED_TRACE(item, k, v)                                                     \
-  do {                                                                              \
-    if (threadIdx.x == 0 && g_mixed_trace != nullptr && (item) < 4096) {            \
-      __builtin_amdgcn_s_waitcnt(0);                                                \
-      g_mixed_trace[((int64_t)blockIdx.y * 4096 + (item)) * 16 + (k)] = (v);        \
-    }                                                                               \
+__shared__ uint64_t sm_mixed_trace[16];
+#define MIXED_TRACE(item, k, v)                      \
+  do {                                               \
+    if (threadIdx.x == 0) sm_mixed_trace[(k)] = (v); \
+  } while (0)
+#define MIXED_TRACE_FLUSH(item)                                                              \
+  do {                                                                                       \
+    if (threadIdx.x == 0 && g_mixed_trace != nullptr && (item) < 4096) {                     \
+      for (int k_ = 0; k_ < 16; ++k_)                                                        \
+        g_mixed_trace[((int64_t)blockIdx.y * 4096 + (item)) * 16 + k_] = sm_mixed_trace[k_]; \
+      for (int k_ = 0; k_ < 16; ++k_)                                                        \
+        if (k_ != 6) sm_mixed_trace[k_] = 0;                                                 \
+    }                                                                                        \
   } while (0)
 #else
 #define MIXED_TRACE(item, k, v) \
+  do {                          \
+  } while (0)
+#define MIXED_TRACE_FLUSH(item) \
   do {                          \
   } while (0)
 #endif
@@ -520,6 +531,7 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   if (tp.n_chunks == 1) {
     __syncthreads();  // LDS is reused by the next item
     MIXED_TRACE(item, 3, __builtin_amdgcn_s_memrealtime());
+    MIXED_TRACE_FLUSH(item);
     return;
   }
   // The last chunk of this (tile, column group) to arrive merges all chunks.
@@ -533,6 +545,7 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   }
   __syncthreads();
   MIXED_TRACE(item, 3, __builtin_amdgcn_s_memrealtime());
+  MIXED_TRACE_FLUSH(item);
 }
 
 // Grid (n_workgroups, H_kv): every workgroup plans the whole batch — per
