@@ -101,15 +101,29 @@ def build_layers(case, dev, R: int, seed: int = 1):
     return layers
 
 
+MAX_GRAPH_CALLS = 4096
+
+
 def time_calls(fn_list, steps: int, warmup: int, use_graph: bool, repeats: int) -> tuple[float, int]:
-    """Median over repeats of the per-call time (us) of running fn_list round-robin."""
+    """Median over repeats of the per-call time (us) of `steps` calls of fn_list, round-robin.
+
+    With graphs, one hipGraph records a timed region's calls — exactly `steps`
+    of them, rotating over fn_list, up to MAX_GRAPH_CALLS; beyond that
+    fn_list is recorded once and replayed (steps rounded up to a multiple of
+    its length).  Before every timed region the same work runs once untimed,
+    so the GPU is busy while the host records the start event and enqueues
+    the timed replays: the region never waits on the host's graph launch.
+    Returns (us per call, calls timed per region)."""
     R = len(fn_list)
-    reps = max(1, -(-steps // R))
-    steps = reps * R
+    if use_graph and steps <= MAX_GRAPH_CALLS:
+        seq, reps = [fn_list[i % R] for i in range(steps)], 1
+    else:
+        seq, reps = fn_list, max(1, -(-steps // R))
+        steps = reps * R
     stream = torch.cuda.current_stream()
 
     def run_all():
-        for f in fn_list:
+        for f in seq:
             f()
 
     if use_graph:
@@ -118,13 +132,14 @@ def time_calls(fn_list, steps: int, warmup: int, use_graph: bool, repeats: int) 
         body = StepGraph(run_all).replay
     else:
         body = run_all
-    for _ in range(max(1, -(-warmup // R))):
+    for _ in range(max(1, -(-warmup // len(seq)))):
         body()
     torch.cuda.synchronize()
     times = []
     for _ in range(repeats):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        body()  # untimed lead: keeps the GPU busy while the timed region is enqueued
         start.record(stream)
         for _ in range(reps):
             body()
