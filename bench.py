@@ -226,7 +226,7 @@ def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chun
 
 
 def bench_kernels(args):
-    """Per-launch times (hipGraph replay of R launches over rotating inputs) of
+    """Per-launch times (one hipGraph of at least 128 launches over rotating inputs) of
     the kernels the drop-in runs besides the headline call: the standalone KV
     appends (decode mode at config 2's B = 32; token mode and the fused
     QKV-split + RoPE + append at config 3's T = 1052) and the rope-mode decode
@@ -636,7 +636,9 @@ def main():
             "pool_pages_per_layer": int(case.k_pool.shape[0]),
             "layer_rotation": R,
             "splits": n_splits,
-            "timing": "hipGraph replay of R calls" if use_graph else "eager launches",
+            "timing": ("one hipGraph of the K timed calls rotating over the layer pools, after an untimed lead replay"
+                       if use_graph and steps <= MAX_GRAPH_CALLS else
+                       "hipGraph replay of the layer rotation" if use_graph else "eager launches"),
             "algorithmic_bytes_per_call": bytes_call,
         },
         "roofline": {
