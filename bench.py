@@ -70,6 +70,8 @@ def parse():
     ap.add_argument("--trace-mixed", action="store_true",
                     help="per-item phase trace of one config-3 mixed launch; needs a trace build "
                          "(-D CIE_MIXED_TRACE, loaded through CIE_PAGED_LIB)")
+    ap.add_argument("--trace-out", default=None, metavar="PATH",
+                    help="with --trace-mixed: also write every item's stamps to PATH as JSON")
     ap.add_argument("--mixed-part", choices=("all", "prefill", "decode"), default="all",
                     help="config 3: time only its prefill chunks or only its decode rows")
     return ap.parse_args()
@@ -430,6 +432,9 @@ def trace_mixed(args):
                   f"{statistics.median(x['start'] for x in sel):6.2f} {med('lookup'):7.2f} {med('q'):6.2f} "
                   f"{med('loop'):7.2f} {med('fold'):6.2f} {med('end'):6.2f} "
                   f"{max(x['end'] - x['start'] for x in sel):8.2f}")
+    if args.trace_out:
+        with open(args.trace_out, "w") as f:
+            json.dump(items, f)
     late = sorted(items, key=lambda x: -x["end"])[:8]
     print("latest items (seq, tile, col tiles, chunks, key tiles: start -> end):")
     for x in late:

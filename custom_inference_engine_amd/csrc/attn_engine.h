@@ -175,6 +175,7 @@ struct SoftmaxAcc {
   float m[NCT];     // reference max (log2 domain), identical across a column's 4 lanes
   float thr[NCT];   // raw score above which m must move: (m + kRescaleSlack) / scale
   f32x4 lsum[NCT];  // [0]: the column's sum of P (an MFMA against ones: no lane reduction)
+  float lpart[NCT];  // or: this lane's part of that sum (the pipelined stream; 4 lanes a column)
   f32x4 acc[NCT][Geo<D>::NT];
 
   __device__ __forceinline__ void init() {
@@ -183,11 +184,13 @@ struct SoftmaxAcc {
       m[c] = kEmptyMax;
       thr[c] = kEmptyMax;
       lsum[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      lpart[c] = 0.f;
 #pragma unroll
       for (int nt = 0; nt < Geo<D>::NT; ++nt) acc[c][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-  __device__ __forceinline__ float l(int c) const { return lsum[c][0]; }
+  // One of the two sums stays zero (constant-folded away by the compiler).
+  __device__ __forceinline__ float l(int c) const { return lsum[c][0] + col_sum4(lpart[c]); }
 };
 
 // The reference max of a column moves only when a step's max exceeds it by
@@ -354,6 +357,8 @@ struct PagedSrc {
   int64_t n_pages;
   int page_size;
   int32_t* err;
+  uint32_t tpp_magic;   // div_magic(page_size / 16) (the mixed kernel's streams)
+  uint32_t pool_bytes;  // each pool's size if under 4 GiB, else 0 (the pipelined stream)
 };
 
 // Stream key tiles [t_begin, t_end) of one wave through attend_pair, two
@@ -395,7 +400,7 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
   auto lane_pages = [&](int c0) {
     int page = 0;
     if (lane < min(kWave, t_end - c0)) {
-      int64_t pg = src.bt_row[(c0 + lane) / tpp];
+      int64_t pg = src.bt_row[magic_div(c0 + lane, src.tpp_magic)];
       if (pg < 0 || pg >= src.n_pages) {
         set_err(src.err, CIE_ERRBIT_PAGE);
         pg = 0;
@@ -407,7 +412,9 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
   // pool element offset of tile c0 + lane (page, head and in-page rows
   // applied), computed once per 64 tiles so a step only reads two lanes
   auto lane_offsets = [&](int c0, int page) {
-    return (int64_t)page * src.page_stride + src.head_off + (int64_t)(((c0 + lane) % tpp) * 16) * D;
+    const int t = c0 + lane;
+    const int in_page = t - magic_div(t, src.tpp_magic) * tpp;
+    return (int64_t)page * src.page_stride + src.head_off + (int64_t)(in_page * 16) * D;
   };
   int page = lane_pages(t_begin);
   prologue();  // while the first page ids are in flight
@@ -449,6 +456,321 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
         issue((u + PF) % (PF + 1), j + PF);
         if (j < n_pairs)
           attend_pair<D, NCT, QS>(st, ring[u], qop, keya[u], keyb[u], lim, mask_from, scale_log2, grp);
+      }
+    }
+  }
+}
+
+// ---- The software-pipelined stream (mixed kernel) ----
+//
+// A wave's 32-key step t is: S(t) = K(t) . Q^T for its column tiles, the
+// reference-max check on S(t), then P(t) = 2^(S(t)*scale - m) and
+// acc += V(t)^T . P(t)^T.  stream_tiles_pipelined puts step t's softmax and
+// P.V and step t+1's S MFMAs in one basic block (they depend on nothing in
+// each other), one MFMA issued between every three VALU instructions; the
+// masking and reference-max check of step t+1 follow in their own short
+// blocks, the rare rescale in a branch.  (A lone wave on a gfx950 SIMD
+// overlaps its own MFMA and VALU work only in part — measured: a step's
+// math alone costs about the sum of its MFMA and VALU parts — so this
+// schedule gains little by itself; the stream's one-descriptor loads gain
+// more.)
+
+// S^T of one step against column tile c: s[t] = K(tile t) . Q(c)^T.
+template <int D, class QS>
+__device__ __forceinline__ void tile_scores(f32x4 (&s)[2], const KVPair<D>& kv, const QS& qop,
+                                            int c) {
+  s[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+  s[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < Geo<D>::KS; ++ks) {
+    const f16x8 qk = qop(c, ks);
+    s[0] = mfma16x16x32(kv.k[0][ks], qk, s[0]);
+    s[1] = mfma16x16x32(kv.k[1][ks], qk, s[1]);
+  }
+}
+
+// Scores of keys at or past each lane's column limit (lim(c): the limit of
+// the lane's column in column tile c) become -inf.
+template <int NCT, class Lim>
+__device__ __forceinline__ void mask_scores(f32x4 (&s)[NCT][2], int key0a, int key0b, const Lim& lim,
+                                            int grp) {
+  const int kba = key0a + 4 * grp;
+  const int kbb = key0b + 4 * grp;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int l = lim(c);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s[c][0][r] = kba + r < l ? s[c][0][r] : kNegInf;
+      s[c][1][r] = kbb + r < l ? s[c][1][r] : kNegInf;
+    }
+  }
+}
+
+// Move the reference max of the column tiles when any lane's raw maximum
+// passed its column's threshold (rare; see kRescaleSlack), rescaling the
+// state.  Every column tile is updated then: its new max is at least the old
+// one, so the rescale factor is at most 1 and o = acc / l is unchanged.
+template <int D, int NCT>
+__device__ __forceinline__ void update_max(SoftmaxAcc<D, NCT>& st, const f32x4 (&s)[NCT][2],
+                                           float scale_log2) {
+  float xb[NCT];
+  bool need = false;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    xb[c] = fmaxf(fmaxf(fmaxf(s[c][0][0], s[c][0][1]), fmaxf(s[c][0][2], s[c][0][3])),
+                  fmaxf(fmaxf(s[c][1][0], s[c][1][1]), fmaxf(s[c][1][2], s[c][1][3])));
+    // (scaled against m, not a stored threshold: a register a column tile less)
+    need |= __builtin_fmaf(xb[c], scale_log2, -st.m[c]) > kRescaleSlack;
+  }
+  if (__any(need)) {
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+      const float m_new = fmaxf(st.m[c], col_max4(xb[c]) * scale_log2);
+      const float alpha = fast_exp2(st.m[c] - m_new);  // 0 for an empty state
+      st.m[c] = m_new;
+      st.lsum[c][0] *= alpha;
+      st.lpart[c] *= alpha;
+#pragma unroll
+      for (int nt = 0; nt < Geo<D>::NT; ++nt) st.acc[c][nt] *= alpha;
+    }
+  }
+}
+
+// The P.V operands of a step: va[nt] holds, for the lane's output dim of
+// d-tile nt, the 8 keys key(grp, e) (a transpose of the loaded V rows).
+template <int D>
+__device__ __forceinline__ void v_operands(f16x8 (&va)[Geo<D>::NT], const KVPair<D>& kv) {
+#pragma unroll
+  for (int nt = 0; nt < Geo<D>::NT; ++nt)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) va[nt][e] = kv.v[e][nt];
+}
+
+// S^T of one step against one column tile whose Q^T operands are in q.
+template <int D>
+__device__ __forceinline__ void tile_scores_q(f32x4 (&s)[2], const KVPair<D>& kv,
+                                              const f16x8 (&q)[Geo<D>::KS]) {
+  s[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+  s[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < Geo<D>::KS; ++ks) {
+    s[0] = mfma16x16x32(kv.k[0][ks], q[ks], s[0]);
+    s[1] = mfma16x16x32(kv.k[1][ks], q[ks], s[1]);
+  }
+}
+
+// P = 2^(s * scale - m) of one column tile, in fp16 (the P.V operand).
+__device__ __forceinline__ f16x8 tile_probs(float m, const f32x4 (&s)[2], float scale_log2) {
+  f16x8 pop;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    pop[r] = (f16)fast_exp2(__builtin_fmaf(s[0][r], scale_log2, -m));
+    pop[4 + r] = (f16)fast_exp2(__builtin_fmaf(s[1][r], scale_log2, -m));
+  }
+  return pop;
+}
+
+// acc += V^T . P^T of column tile c, and the lane's part of the row sums
+// += its 8 fp16 P values (v_dot2_f32_f16 against (1, 1): exact products,
+// fp32 sums; one register a column tile instead of an MFMA output's four).
+template <int D, int NCT>
+__device__ __forceinline__ void accumulate_probs(SoftmaxAcc<D, NCT>& st, int c, const f16x8& pop,
+                                                 const f16x8 (&va)[Geo<D>::NT]) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 one2 = {(f16)1.f, (f16)1.f};
+#pragma unroll
+  for (int nt = 0; nt < Geo<D>::NT; ++nt) st.acc[c][nt] = mfma16x16x32(va[nt], pop, st.acc[c][nt]);
+  float l = st.lpart[c];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) l = __builtin_amdgcn_fdot2(h2{pop[2 * i], pop[2 * i + 1]}, one2, l, false);
+  st.lpart[c] = l;
+}
+
+// 1: interleave each segment's MFMAs one at a time with its VALU work
+#ifndef CIE_STEP_INTERLEAVE
+#define CIE_STEP_INTERLEAVE 1
+#endif
+
+// stream_tiles with steps overlapped as described above.  Step t's V rows
+// are loaded at the start of step t-1 and its K tiles at the start of step
+// t-2, so K (needed mid-step, for the S MFMAs one step ahead) has one and a
+// half steps of lead and V one.
+//
+// Loads go through one descriptor per pool (the pool is under 4 GiB: the
+// caller checks) with the tile's byte offset as the scalar offset: a step
+// costs two v_readlane and no per-tile descriptor (a per-tile descriptor is
+// about 17 scalar instructions, which a lone wave per SIMD pays in issue
+// slots).  Rows past key_end are then real pool memory: their scores are
+// masked like any key past a column's limit, and their V rows are zeroed in
+// registers on the steps that hold them (pool memory past a sequence's end
+// may hold anything).  Past the last step the loads repeat the last step's
+// tiles (cache hits), so every step issues the same loads and each wait
+// covers exactly the step it is for.
+template <int D, int NCT, class QS, class Lim, class Prologue>
+__device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, const QS& qop,
+                                                       const Lim& lim, int t_begin,
+                                                       int t_end, int key_end,
+                                                       const PagedSrc& src, float scale_log2,
+                                                       int r16, int grp, Prologue prologue) {
+  constexpr int NT = Geo<D>::NT;
+  typedef typename HVec<NT>::type vrow_t;
+  t_begin = uniform(t_begin);
+  t_end = uniform(t_end);
+  key_end = uniform(key_end);
+  if (t_begin >= t_end) {
+    prologue();
+    return;
+  }
+  int mask_from = kNoKey;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) mask_from = min(mask_from, lim(c));
+  for (int off = 1; off < kWave; off <<= 1) mask_from = min(mask_from, __shfl_xor(mask_from, off, kWave));
+  mask_from = uniform(mask_from);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int tpp = src.page_size >> 4;
+  const TileLaneOffsets<D> lanes(r16, grp);
+  const __amdgpu_buffer_rsrc_t kd = coherent_rsrc(src.k_pool, src.pool_bytes);
+  const __amdgpu_buffer_rsrc_t vd = coherent_rsrc(src.v_pool, src.pool_bytes);
+  auto lane_pages = [&](int c0) {
+    int page = 0;
+    if (lane < min(kWave, t_end - c0)) {
+      int64_t pg = src.bt_row[magic_div(c0 + lane, src.tpp_magic)];
+      if (pg < 0 || pg >= src.n_pages) {
+        set_err(src.err, CIE_ERRBIT_PAGE);
+        pg = 0;
+      }
+      page = (int)pg;
+    }
+    return page;
+  };
+  // byte offset in the pool of tile c0 + lane (page, head and in-page rows)
+  auto lane_offsets = [&](int c0, int page) {
+    const int t = c0 + lane;
+    const int in_page = t - magic_div(t, src.tpp_magic) * tpp;
+    return (uint32_t)(((int64_t)page * src.page_stride + src.head_off + (int64_t)(in_page * 16) * D) * 2);
+  };
+  int page = lane_pages(t_begin);
+  prologue();
+  for (int c0 = t_begin; c0 < t_end; c0 += kWave) {
+    const int n_chunk = min(kWave, t_end - c0);
+    if (c0 != t_begin) page = lane_pages(c0);
+    const uint32_t toff = lane_offsets(c0, page);
+    const int n_pairs = (n_chunk + 1) >> 1;
+    KVPair<D> ring[3];  // K in slot t % 3, V in slot t % 2
+    // byte offsets of step j's two tiles (a missing second tile: the first
+    // again, its keys masked and its V rows zeroed)
+    auto offsets = [&](int j, uint32_t& oa, uint32_t& ob) {
+      const int ka = 2 * min(j, n_pairs - 1);
+      oa = __builtin_amdgcn_readlane(toff, ka);
+      ob = ka + 1 < n_chunk ? __builtin_amdgcn_readlane(toff, ka + 1) : oa;
+    };
+    // (the lane offsets pass through an empty asm at each use, so the
+    // compiler cannot hoist "offset + constant" out of the loop into extra
+    // registers; the constants then go into the loads' immediate offsets)
+    auto issue_k = [&](int slot, int j) {
+      uint32_t o[2];
+      offsets(j, o[0], o[1]);
+      uint32_t ko = lanes.k;
+      asm volatile("" : "+v"(ko));
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int ks = 0; ks < Geo<D>::KS; ++ks)
+          ring[slot].k[t][ks] =
+              __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(kd, ko + 64 * ks, o[t], 0));
+    };
+    auto issue_v = [&](int slot, int j) {
+      uint32_t o[2];
+      offsets(j, o[0], o[1]);
+      uint32_t vo = lanes.v;
+      asm volatile("" : "+v"(vo));
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (NT == 4)
+            ring[slot].v[4 * t + e] = __builtin_bit_cast(
+                vrow_t, __builtin_amdgcn_raw_buffer_load_b64(vd, vo + e * D * 2, o[t], 0));
+          else
+            ring[slot].v[4 * t + e] = __builtin_bit_cast(
+                vrow_t, __builtin_amdgcn_raw_buffer_load_b128(vd, vo + e * D * 2, o[t], 0));
+        }
+    };
+    auto step_keys = [&](int j, int& ka, int& kb) {
+      const int a = 2 * min(j, n_pairs - 1);
+      ka = (c0 + a) * 16;
+      kb = a + 1 < n_chunk ? ka + 16 : kNoKey;
+    };
+    issue_k(0, 0);
+    issue_v(0, 0);
+    issue_k(1, 1);
+    f32x4 s[NCT][2];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) tile_scores<D>(s[c], ring[0], qop, c);
+    {
+      int ka, kb;
+      step_keys(0, ka, kb);
+      if (max(ka, kb) + 16 > mask_from) mask_scores<NCT>(s, ka, kb, lim, grp);
+    }
+    update_max<D, NCT>(st, s, scale_log2);
+    for (int j0 = 0; j0 < n_pairs; j0 += 6) {
+#pragma unroll
+      for (int u = 0; u < 6; ++u) {
+        const int j = j0 + u;
+        if (j < n_pairs) {
+          {
+            int ka, kb;
+            step_keys(j, ka, kb);
+            if (max(ka, kb) + 16 > key_end) zero_tail_rows<D>(ring[u % 2], ka, kb, key_end, grp);
+          }
+          f16x8 va[NT];
+          v_operands<D>(va, ring[u % 2]);
+          issue_v((u + 1) % 2, j + 1);
+          issue_k((u + 2) % 3, j + 2);
+          // Segment c: the exponentials of column tile c, the P.V MFMAs of
+          // tile c - 1 and the S MFMAs of tile c for the next step.
+          // Scheduling barriers between segments keep each step's scores
+          // consumed as the next step's are produced (registers); inside a
+          // segment the MFMAs are issued one at a time between VALU
+          // instructions.
+          f32x4 s1[NCT][2];
+          f16x8 pprev;
+#pragma unroll
+          for (int c = 0; c <= NCT; ++c) {
+            __builtin_amdgcn_sched_barrier(0);
+            f16x8 q[Geo<D>::KS];
+            if (c < NCT) {
+#pragma unroll
+              for (int ks = 0; ks < Geo<D>::KS; ++ks) q[ks] = qop(c, ks);
+            }
+            f16x8 pc;
+            if (c < NCT) pc = tile_probs(st.m[c], s[c], scale_log2);
+            if (c > 0) accumulate_probs<D, NCT>(st, c - 1, pprev, va);
+            if (c < NCT) tile_scores_q<D>(s1[c], ring[(u + 1) % 3], q);
+            pprev = pc;
+            if (CIE_STEP_INTERLEAVE && c > 0 && c < NCT) {
+              __builtin_amdgcn_sched_group_barrier(0x100, 2 * Geo<D>::KS, 0);  // Q reads
+#pragma unroll
+              for (int i = 0; i < NT + 2 * Geo<D>::KS; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+              }
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          if (j + 1 < n_pairs) {
+            int ka, kb;
+            step_keys(j + 1, ka, kb);
+            if (max(ka, kb) + 16 > mask_from) mask_scores<NCT>(s1, ka, kb, lim, grp);
+            update_max<D, NCT>(st, s1, scale_log2);
+          }
+#pragma unroll
+          for (int c = 0; c < NCT; ++c) {
+            s[c][0] = s1[c][0];
+            s[c][1] = s1[c][1];
+          }
+        }
       }
     }
   }

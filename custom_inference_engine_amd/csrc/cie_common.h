@@ -186,6 +186,25 @@ __device__ __forceinline__ bool arrive_last(int32_t* arrival, int64_t n_words, i
 }
 
 
+// floor(x / d) for x * d < 2^31 as one multiply-high: magic = ceil(2^31 / d)
+// (div_magic, computed on the host, so the kernel holds no per-lane
+// reciprocal registers for a run-time divisor): 2x * magic / 2^32 =
+// x / d + x * r / (d * 2^31) with r < d, whose floor is x / d exactly.
+__device__ __forceinline__ int magic_div(int x, uint32_t magic) {
+  return (int)__umulhi((uint32_t)x << 1, magic);
+}
+static inline uint32_t div_magic(uint32_t d) {
+  return (uint32_t)((((uint64_t)1 << 31) + d - 1) / d);
+}
+
+// A value the compiler must treat as unknown at this point: what is derived
+// from it is computed here, not hoisted to the kernel's start and held in
+// registers across the hot loops.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Uniform (wave-invariant) value hint: lets the compiler keep it in an SGPR.
 __device__ __forceinline__ int uniform(int x) {
   return __builtin_amdgcn_readfirstlane(x);

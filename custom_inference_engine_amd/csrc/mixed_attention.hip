@@ -63,6 +63,9 @@ namespace cie {
 #ifndef CIE_MIXED_WG_PER_CU
 #define CIE_MIXED_WG_PER_CU 1
 #endif
+#ifndef CIE_MIXED_PIPELINED
+#define CIE_MIXED_PIPELINED 1
+#endif
 #ifndef CIE_MIXED_NARROW_PAIRS
 #define CIE_MIXED_NARROW_PAIRS 8
 #endif
@@ -83,6 +86,13 @@ constexpr int mixed_waves() {
 template <int D>
 constexpr int col_group() {
   return D <= 64 ? CIE_MIXED_CG : 1;
+}
+// The key stream of a work item of several column tiles at D = 64, when the
+// pools are under 4 GiB: stream_tiles_pipelined (steps overlapped, one
+// descriptor per pool); otherwise stream_tiles.
+template <int D>
+constexpr bool mixed_pipelined() {
+  return D == 64 && CIE_MIXED_PIPELINED;
 }
 template <int D>
 constexpr int mixed_pf() {
@@ -110,6 +120,8 @@ struct MixedParams {
   int32_t* counters;  // 2 x [B][H_kv][n_qtiles][kMaxColGroups]: arrival words, then stale words
   int64_t pool_page_stride, pool_head_stride, bt_stride, n_pages, total_T;
   int32_t bt_width, n_slots, B, H_q, H_kv, G, page_size, n_qtiles;
+  uint32_t g_magic, tpp_magic;  // div_magic(G), div_magic(page_size / 16)
+  uint32_t pool_bytes;          // bytes of each pool if under 4 GiB, else 0
   float scale_log2;
   int32_t* err;
 };
@@ -185,7 +197,7 @@ __device__ __forceinline__ void load_combo_q(const MixedParams& p, const SeqInfo
                                              f16x8 (&qop)[Geo<D>::KS], int& lim) {
   const int cc = ct * 16 + r16;
   if (cc < tp.n_combos) {
-    const int row = cc / p.G;
+    const int row = magic_div(cc, p.g_magic);
     const int head = cc - row * p.G;
     const f16* qrow =
         p.q + ((s.t0 + tp.row0 + row) * p.H_q + g * p.G + head) * (int64_t)D + 8 * grp;
@@ -203,14 +215,14 @@ __device__ __forceinline__ void load_combo_q(const MixedParams& p, const SeqInfo
 __device__ __forceinline__ int combo_lim(const MixedParams& p, const SeqInfo& s,
                                          const TilePlan& tp, int ct, int r16) {
   const int cc = ct * 16 + r16;
-  return cc < tp.n_combos ? s.c + tp.row0 + cc / p.G + 1 : tp.key_end;
+  return cc < tp.n_combos ? s.c + tp.row0 + magic_div(cc, p.g_magic) + 1 : tp.key_end;
 }
 
 // Row of column cc of the tile relative to the tile's first row's first q
 // head, in units of (row, q head) = H_q * (row) + g * G + head - ...; i.e. the
 // index into [(t0 + row0) * H_q, ...) of the tile's partial / output rows.
 __device__ __forceinline__ int column_off(const MixedParams& p, int g, int cc) {
-  const int row = cc / p.G;
+  const int row = magic_div(cc, p.g_magic);
   const int head = cc - row * p.G;
   return row * p.H_q + g * p.G + head;
 }
@@ -268,7 +280,7 @@ __device__ __forceinline__ PartRegion part_region(const MixedParams& p, const Se
 // One work item's waves: key tiles [w0, w1) against column tiles
 // [ct0, ct0 + NCT); then the workgroup folds each column tile through LDS
 // and writes o (single chunk) or the chunk's partial state.
-template <int D, int NCT>
+template <int D, bool P32, int NCT>
 __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s,
                                           const TilePlan& tp, int g, int ct0, int chunk, int w0,
                                           int w1, const PagedSrc& src, int wave, int r16, int grp,
@@ -292,7 +304,7 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
     for (int c = 0; c < NCT; ++c) lim[c] = combo_lim(p, s, tp, ct0 + c, r16);
     const bool loads = wave < NCT;
     if (loads) load_combo_q<D>(p, s, tp, g, ct0 + wave, r16, grp, qw, lim_w);
-    const int lane = threadIdx.x & (kWave - 1);
+    const int lane = opaque((int)threadIdx.x) & (kWave - 1);
     auto stage_q = [&]() {
       if (loads) {
 #pragma unroll
@@ -301,8 +313,20 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
       __syncthreads();
       MIXED_TRACE(item, 9, __builtin_amdgcn_s_memrealtime());
     };
-    stream_tiles<D, NCT, mixed_pf<D>()>(st, QLds<D>{sm_q, lane}, lim, w0, w1, tp.key_end, src,
-                                        p.scale_log2, r16, grp, stage_q);
+    // the lane's column limits, as row offsets (< 16) packed a byte per
+    // column tile over one base: a register, not NCT (read only on the
+    // masked steps)
+    uint32_t rows = 0;
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) rows |= (uint32_t)(lim[c] - (s.c + tp.row0 + 1)) << (8 * c);
+    const int lim_base = uniform(s.c + tp.row0 + 1);
+    auto lims = [&](int c) { return lim_base + (int)((rows >> (8 * c)) & 0xffu); };
+    if constexpr (P32 && mixed_pipelined<D>() && NCT >= 2)
+      stream_tiles_pipelined<D, NCT>(st, QLds<D>{sm_q, lane}, lims, w0, w1, tp.key_end, src,
+                                     p.scale_log2, r16, grp, stage_q);
+    else
+      stream_tiles<D, NCT, mixed_pf<D>()>(st, QLds<D>{sm_q, lane}, lim, w0, w1, tp.key_end, src,
+                                          p.scale_log2, r16, grp, stage_q);
   } else {
     f16x8 qop[NCT][KS];
     int lim[NCT];
@@ -324,7 +348,11 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
   // 109 KB cost 12 %.)
   static_assert(NCT <= W, "a wave per column tile of the group");
   constexpr int FT = fold_tiles<D>();
-  const int lane = threadIdx.x & (kWave - 1);
+  // lane ids derived afresh: nothing lane-dependent of the fold is held in
+  // registers through the key loop
+  const int lane = opaque((int)threadIdx.x) & (kWave - 1);
+  r16 = lane & 15;
+  grp = lane >> 4;
   const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
   const PartRegion pr = part_region<D>(p, s, tp);
 #pragma unroll
@@ -421,7 +449,7 @@ __device__ __forceinline__ void merge_group(const MixedParams& p, const SeqInfo&
   const int K = tp.n_chunks;
   const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
   const PartRegion pr = part_region<D>(p, s, tp);
-  for (int it = threadIdx.x; it < n_cols * (D / 4); it += mixed_waves<D>() * kWave) {
+  for (int it = opaque((int)threadIdx.x); it < n_cols * (D / 4); it += mixed_waves<D>() * kWave) {
     const int j = it / (D / 4);
     const int d = (it - j * (D / 4)) * 4;
     const int off = column_off(p, g, ct0 * 16 + j);
@@ -488,15 +516,15 @@ __device__ __forceinline__ int seq_items(const SeqInfo& s, int n_qtiles, int G) 
 
 // One work item: column group gi, chunk `chunk` of query tile qt of sequence
 // b, kv head g.
-template <int D>
+template <int D, bool P32>
 __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo& s, int b, int g,
                                              int qt, int j, f32x4* sm_facc, float2* sm_fml,
-                                             f16x8* sm_q, int* sm_last,
-                                             int item) {
+                                             f16x8* sm_q, int* sm_last, int item) {
   constexpr int CG = col_group<D>();
   constexpr int W = mixed_waves<D>();
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = uniform(threadIdx.x / kWave);
+  const int tid = opaque((int)threadIdx.x);
+  const int lane = tid & (kWave - 1);
+  const int wave = uniform(tid / kWave);
   const int r16 = lane & 15;
   const int grp = lane >> 4;
   const TilePlan tp = tile_plan<CG, W>(qt, s, p.G);
@@ -510,13 +538,13 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   split_steps(kt0, kt1, wave, W, w0, w1);
   const PagedSrc src{p.k_pool,  p.v_pool,  p.block_table + s.slot * p.bt_stride,
                      (int64_t)g * p.pool_head_stride, p.pool_page_stride, p.n_pages,
-                     p.page_size, p.err};
+                     p.page_size, p.err, p.tpp_magic, p.pool_bytes};
   switch (n) {
 #define CIE_GROUP_CASE(k)                                                                      \
   case k:                                                                                      \
     if constexpr (k <= CG)                                                                     \
-      run_group<D, k>(p, s, tp, g, ct0, chunk, w0, w1, src, wave, r16, grp, sm_facc, sm_fml, \
-                      sm_q, item);                                                             \
+      run_group<D, P32, k>(p, s, tp, g, ct0, chunk, w0, w1, src, wave, r16, grp, sm_facc,     \
+                           sm_fml, sm_q, item);                                               \
     break;
     CIE_GROUP_CASE(1)
     CIE_GROUP_CASE(2)
@@ -559,7 +587,7 @@ constexpr int mixed_waves_per_simd() {
   return D <= 64 && (col_group<D>() <= 2 || CIE_MIXED_QLDS) ? 2 : 1;
 }
 
-template <int D>
+template <int D, bool P32>
 __global__ __launch_bounds__(mixed_waves<D>() * kWave)
 __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_attention_kernel(
     MixedParams p) {
@@ -659,7 +687,8 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     }
     MIXED_TRACE(item, 1, __builtin_amdgcn_s_memrealtime());
     MIXED_TRACE(item, 7, (uint64_t)(b * 1000 + qt));
-    process_item<D>(p, s, b, g, uniform(qt), uniform(j), sm_facc, sm_fml, sm_q, &sm_last, item);
+    process_item<D, P32>(p, s, b, g, uniform(qt), uniform(j), sm_facc, sm_fml, sm_q, &sm_last,
+                         item);
   }
 }
 
@@ -675,8 +704,12 @@ static int mixed_workgroups(int H_kv) {
 template <int D>
 static int launch_mixed(const MixedParams& p, hipStream_t stream) {
   dim3 grid(mixed_workgroups(p.H_kv), p.H_kv, 1);
-  hipLaunchKernelGGL((mixed_attention_kernel<D>), grid, dim3(mixed_waves<D>() * kWave),
-                     mixed_plan_lds(p.B), stream, p);
+  if (p.pool_bytes != 0)
+    hipLaunchKernelGGL((mixed_attention_kernel<D, true>), grid, dim3(mixed_waves<D>() * kWave),
+                       mixed_plan_lds(p.B), stream, p);
+  else
+    hipLaunchKernelGGL((mixed_attention_kernel<D, false>), grid, dim3(mixed_waves<D>() * kWave),
+                       mixed_plan_lds(p.B), stream, p);
   return (int)hipGetLastError();
 }
 
@@ -741,6 +774,7 @@ extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, c
   // region (16 * H_q rows of kMaxChunks * D floats) must fit in 31 bits
   if (G > 8 || page_size % 16 != 0 || B > kMaxSeqs || H_kv > 65535 ||
       n_qtiles > 0x7fffffff || bt_width * page_size > 0x7fffffff ||
+      (bt_width * page_size / 16) * (page_size / 16) > 0x7fffffff ||  // magic_div of tile ids
       total_T * kMaxColGroups * kMaxChunks > 0x7fffffff ||
       16 * H_q * kMaxChunks * D * 4 > 0x7fffffff)
     return CIE_EUNSUPPORTED;
@@ -779,6 +813,10 @@ extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, c
   p.G = (int32_t)G;
   p.page_size = (int32_t)page_size;
   p.n_qtiles = (int32_t)n_qtiles;
+  p.g_magic = div_magic((uint32_t)G);
+  const int64_t pool_bytes = n_pages * pool_page_stride * 2;
+  p.pool_bytes = pool_bytes < ((int64_t)1 << 32) ? (uint32_t)pool_bytes : 0u;
+  p.tpp_magic = div_magic((uint32_t)(page_size / 16));
   p.scale_log2 = kLog2e / __builtin_sqrtf((float)D);
   p.err = err;
   hipStream_t st = static_cast<hipStream_t>(stream);

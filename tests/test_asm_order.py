@@ -65,23 +65,36 @@ def _kernels(asm: str) -> dict[str, list[str]]:
 
 
 def _check_arrival(name: str, body: list[str]) -> None:
-    atom = next((i for i, l in enumerate(body) if ATOMIC_RET.match(l)), None)
-    assert atom is not None, f"{name}: no arrival atomic"
-    waited = False
-    for line in reversed(body[:atom]):
-        if WAIT_VM0.match(line):
-            waited = True
-        if STORE.match(line):
-            assert waited, f"{name}: a store before the arrival atomic is not waited for: {line.strip()}"
-            break
-    else:
-        pytest.fail(f"{name}: no partial store before the arrival atomic")
-    # the merge reads partials with sc1 loads, after waiting for the atomic's value
-    later = body[atom + 1:]
-    first_load = next((i for i, l in enumerate(later) if SC1_LOAD.match(l)), None)
-    assert first_load is not None, f"{name}: no sc1 partial loads after the arrival"
-    assert any(WAIT_VM0.match(l) for l in later[:first_load]), \
-        f"{name}: partial loads issued before the arrival atomic returned"
+    """Every arrival atomic — a returning atomic add whose winner path reads
+    partials with sc1 loads before the next returning atomic — waits for the
+    stores issued since the previous atomic (vmcnt(0) after the last of them),
+    and the partial loads after it wait for its value.  Returning atomics with
+    no sc1 loads after them (a work queue's fetch) publish nothing and are not
+    held to this."""
+    atoms = [i for i, l in enumerate(body) if ATOMIC_RET.match(l)]
+    assert atoms, f"{name}: no returning atomic"
+    arrivals = []
+    for k, a in enumerate(atoms):
+        end = atoms[k + 1] if k + 1 < len(atoms) else len(body)
+        if any(SC1_LOAD.match(l) for l in body[a + 1:end]):
+            arrivals.append((k, a))
+    assert arrivals, f"{name}: no arrival atomic"
+    stores_checked = 0
+    for k, a in arrivals:
+        # the last store before the arrival must be complete before the first
+        # returning atomic after it (the arrival, or a stale-path atomic laid
+        # out ahead of it)
+        last = max((i for i in range(a) if STORE.match(body[i])), default=None)
+        if last is not None:
+            first_atom = min(i for i in atoms if i > last)
+            assert any(WAIT_VM0.match(l) for l in body[last + 1:first_atom]), \
+                f"{name}: a store before the arrival atomic is not waited for: {body[last].strip()}"
+            stores_checked += 1
+        later = body[a + 1:]
+        first_load = next(i for i, l in enumerate(later) if SC1_LOAD.match(l))
+        assert any(WAIT_VM0.match(l) for l in later[:first_load]), \
+            f"{name}: partial loads issued before the arrival atomic returned"
+    assert stores_checked, f"{name}: no partial store before an arrival atomic"
 
 
 @pytest.mark.parametrize("src,kernel", [("paged_decode.hip", "decode_kernel"),
