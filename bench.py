@@ -70,6 +70,8 @@ def parse():
     ap.add_argument("--trace-mixed", action="store_true",
                     help="per-item phase trace of one config-3 mixed launch; needs a trace build "
                          "(-D CIE_MIXED_TRACE, loaded through CIE_PAGED_LIB)")
+    ap.add_argument("--step-probe", action="store_true",
+                    help="time the mixed kernel's step math alone (MFMA / VALU split, 1 and 2 waves per SIMD)")
     ap.add_argument("--trace-out", default=None, metavar="PATH",
                     help="with --trace-mixed: also write every item's stamps to PATH as JSON")
     ap.add_argument("--mixed-part", choices=("all", "prefill", "decode"), default="all",
@@ -194,6 +196,9 @@ def bench_lib():
         p, i64 = ctypes.c_void_p, ctypes.c_int64
         lib.cie_bench_gather_read.restype = ctypes.c_int
         lib.cie_bench_gather_read.argtypes = [p, p, i64, i64, i64, p, p]
+        lib.cie_bench_step_probe.restype = ctypes.c_int
+        lib.cie_bench_step_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.POINTER(ctypes.c_float)]
         _bench_lib = lib
     return _bench_lib
 
@@ -463,6 +468,27 @@ def copy_calibration(args):
     print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
 
 
+def step_probe(args):
+    """The mixed kernel's 32-key step math (4 column tiles, D = 64) with no memory
+    traffic: the whole step, its MFMAs alone and its softmax VALU work alone with
+    one wave per SIMD, and the whole step with two waves per SIMD (time per step of
+    one wave; per SIMD, two waves finish two steps in that time)."""
+    import ctypes
+
+    torch.cuda.init()
+    lib = bench_lib()
+    for mode, wps, what in ((0, 1, "whole step"), (1, 1, "32 MFMAs alone"),
+                            (2, 1, "softmax VALU work alone"), (0, 2, "whole step, 2 waves per SIMD")):
+        us = ctypes.c_float()
+        rc = lib.cie_bench_step_probe(mode, wps, 2000, ctypes.byref(us))
+        if rc != 0:
+            raise RuntimeError(f"cie_bench_step_probe failed: status {rc}")
+        per_simd = us.value / wps
+        print(json.dumps({"probe": "mixed step math", "what": what, "waves_per_simd": wps,
+                          "us_per_step_per_wave": round(us.value, 4),
+                          "us_per_step_per_simd": round(per_simd, 4)}), flush=True)
+
+
 def probe_sweep(args):
     """The gather probe's time per launch by read volume (2 KiB chunks) and by chunk
     size (64 MB): separates its fixed cost from the DRAM rate of shuffled chunks.
@@ -495,6 +521,8 @@ def main():
         return probe_sweep(args)
     if args.kernels:
         return bench_kernels(args)
+    if args.step_probe:
+        return step_probe(args)
     if args.trace_decode:
         return trace_decode(args)
     if args.trace_mixed:

@@ -28,7 +28,7 @@ LIB_NAME = "libcie_paged.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 SOURCES = ("capi.hip", "kv_append.hip", "paged_decode.hip", "mixed_attention.hip")
 # bench.py's measurement helpers: a library of their own, never linked into the product
-BENCH_SOURCES = ("bench/gather_probe.hip",)
+BENCH_SOURCES = ("bench/gather_probe.hip", "bench/step_probe.hip")
 BENCH_LIB_PATH = os.path.join(PKG_DIR, "libcie_bench.so")
 ARCH = "gfx950"
 

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(native_lib):
     # and the ctypes table covers the same set, so every entry point is typed
     assert set(_native._SIGNATURES) == set(declared_functions())
     # bench.py's measurement kernels live in a library of their own
-    for name in ("cie_bench_gather_read", "cie_probe_gather_read"):
+    for name in ("cie_bench_gather_read", "cie_probe_gather_read", "cie_bench_step_probe"):
         assert not hasattr(native_lib, name), name
 
 
