@@ -361,6 +361,21 @@ struct PagedSrc {
   uint32_t pool_bytes;  // each pool's size if under 4 GiB, else 0 (the pipelined stream)
 };
 
+// Page id of key tile c0 + lane of a wave's tiles [.., t_end) (0 for lanes past
+// t_end; a page id outside the pool is reported and read as page 0).
+__device__ __forceinline__ int lane_page_id(const PagedSrc& src, int c0, int t_end, int lane) {
+  int page = 0;
+  if (lane < min(kWave, t_end - c0)) {
+    int64_t pg = src.bt_row[magic_div(c0 + lane, src.tpp_magic)];
+    if (pg < 0 || pg >= src.n_pages) {
+      set_err(src.err, CIE_ERRBIT_PAGE);
+      pg = 0;
+    }
+    page = (int)pg;
+  }
+  return page;
+}
+
 // Stream key tiles [t_begin, t_end) of one wave through attend_pair, two
 // tiles per step.  The page ids of up to 64 tiles are gathered first, one per
 // lane, so a step's K/V loads depend on no other load; a ring of PF + 1
@@ -397,18 +412,7 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
   const int tpp = src.page_size >> 4;  // 16-key tiles per page
   const TileLaneOffsets<D> lanes(r16, grp);
   // page ids of tiles c0 + lane, one per lane
-  auto lane_pages = [&](int c0) {
-    int page = 0;
-    if (lane < min(kWave, t_end - c0)) {
-      int64_t pg = src.bt_row[magic_div(c0 + lane, src.tpp_magic)];
-      if (pg < 0 || pg >= src.n_pages) {
-        set_err(src.err, CIE_ERRBIT_PAGE);
-        pg = 0;
-      }
-      page = (int)pg;
-    }
-    return page;
-  };
+  auto lane_pages = [&](int c0) { return lane_page_id(src, c0, t_end, lane); };
   // pool element offset of tile c0 + lane (page, head and in-page rows
   // applied), computed once per 64 tiles so a step only reads two lanes
   auto lane_offsets = [&](int c0, int page) {
@@ -632,18 +636,7 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
   const TileLaneOffsets<D> lanes(r16, grp);
   const __amdgpu_buffer_rsrc_t kd = coherent_rsrc(src.k_pool, src.pool_bytes);
   const __amdgpu_buffer_rsrc_t vd = coherent_rsrc(src.v_pool, src.pool_bytes);
-  auto lane_pages = [&](int c0) {
-    int page = 0;
-    if (lane < min(kWave, t_end - c0)) {
-      int64_t pg = src.bt_row[magic_div(c0 + lane, src.tpp_magic)];
-      if (pg < 0 || pg >= src.n_pages) {
-        set_err(src.err, CIE_ERRBIT_PAGE);
-        pg = 0;
-      }
-      page = (int)pg;
-    }
-    return page;
-  };
+  auto lane_pages = [&](int c0) { return lane_page_id(src, c0, t_end, lane); };
   // byte offset in the pool of tile c0 + lane (page, head and in-page rows)
   auto lane_offsets = [&](int c0, int page) {
     const int t = c0 + lane;

@@ -239,6 +239,11 @@ __shared__ uint64_t sm_mixed_trace[16];
   do {                                               \
     if (threadIdx.x == 0) sm_mixed_trace[(k)] = (v); \
   } while (0)
+// every wave's first lane (slots 10 + wave: the waves' key-loop ends)
+#define MIXED_TRACE_WAVE(k, v)                                                         \
+  do {                                                                                 \
+    if ((threadIdx.x & (kWave - 1)) == 0) sm_mixed_trace[(k) + threadIdx.x / kWave] = (v); \
+  } while (0)
 #define MIXED_TRACE_FLUSH(item)                                                              \
   do {                                                                                       \
     if (threadIdx.x == 0 && g_mixed_trace != nullptr && (item) < 4096) {                     \
@@ -251,6 +256,9 @@ __shared__ uint64_t sm_mixed_trace[16];
 #else
 #define MIXED_TRACE(item, k, v) \
   do {                          \
+  } while (0)
+#define MIXED_TRACE_WAVE(k, v) \
+  do {                         \
   } while (0)
 #define MIXED_TRACE_FLUSH(item) \
   do {                          \
@@ -337,6 +345,7 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
                                         p.scale_log2, r16, grp, [] {});
   }
   MIXED_TRACE(item, 8, __builtin_amdgcn_s_memrealtime());
+  MIXED_TRACE_WAVE(10, __builtin_amdgcn_s_memrealtime());
   // Fold the waves' states, kFoldTiles column tiles per round: every wave
   // puts its states of the round's column tiles into LDS in its register
   // layout, and after a barrier wave c combines column tile c lane by lane —

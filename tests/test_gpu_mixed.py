@@ -95,6 +95,47 @@ def test_mixed_batch_above_the_plan_limit_is_rejected(native_lib):
                             c.block_table)
 
 
+@pytest.mark.parametrize("n_pages,where", [
+    (2**20 - 1, "top"),    # pools of 4 GiB - 4 KiB: one descriptor per pool, offsets near 2^32
+    (2**20 + 64, "top"),   # pools past 4 GiB: the per-tile descriptor path, offsets past 2^32
+], ids=["just-under-4GiB", "past-4GiB"])
+def test_mixed_pools_near_and_past_4gib(native_lib, n_pages, where):
+    """The kernel streams K/V through one descriptor per pool with 32-bit tile
+    offsets when a pool is under 4 GiB and through per-tile descriptors
+    otherwise; a case's pages placed at the top of such pools read the same
+    keys as the small pool they came from."""
+    case = inputs.make_case([3000, 0, 700, 40], [1, 45, 20, 3], seed=41)
+    note(f"mixed pools of {n_pages} pages ({where})")
+    kp_small, vp_small = case.appended_pools()
+    n_small = kp_small.shape[0]
+    shift = n_pages - n_small  # the case's page p lands at page p + shift
+    kp = torch.empty((n_pages,) + tuple(kp_small.shape[1:]), dtype=torch.float16, device=DEV)
+    vp = torch.empty_like(kp)
+    kp[shift:] = kp_small.to(DEV)
+    vp[shift:] = vp_small.to(DEV)
+    c = case.to(DEV)
+    bt = c.block_table + shift
+    lib = _native.load()
+    H_q, D = 14, 64
+    o = torch.empty_like(c.q)
+    ws = torch.empty(lib.cie_mixed_partials_bytes(case.T, H_q, D), dtype=torch.uint8, device=DEV)
+    max_seqlen = int(case.new_lens.max())
+    ctr = torch.zeros(lib.cie_mixed_counters(case.B, 2, max_seqlen), dtype=torch.int32, device=DEV)
+    err = err_word()
+    rc = lib.cie_mixed_attention(o.data_ptr(), c.q.data_ptr(), kp.data_ptr(), vp.data_ptr(),
+                                 c.cu_seqlens.data_ptr(), c.kv_lens.data_ptr(), c.slot_ids.data_ptr(),
+                                 bt.data_ptr(), ws.data_ptr(), ctr.data_ptr(), case.B, case.T,
+                                 max_seqlen, H_q, 2, D,
+                                 16, n_pages, kp.stride(0), kp.stride(1), bt.stride(0),
+                                 bt.shape[1], bt.shape[0], err.data_ptr(),
+                                 _native.stream_handle(torch.device(DEV)))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    del kp, vp
+    _check(case, o[0].float().cpu(), f"pools of {n_pages} pages")
+
+
 def test_mixed_partials_above_2gib_in_the_low_address_word(native_lib):
     """Split tiles store partials through buffer descriptors built from the region's address.
 
