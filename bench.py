@@ -197,7 +197,7 @@ def bench_lib():
         lib.cie_bench_gather_read.restype = ctypes.c_int
         lib.cie_bench_gather_read.argtypes = [p, p, i64, i64, i64, p, p]
         lib.cie_bench_step_probe.restype = ctypes.c_int
-        lib.cie_bench_step_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        lib.cie_bench_step_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                              ctypes.POINTER(ctypes.c_float)]
         _bench_lib = lib
     return _bench_lib
@@ -478,16 +478,20 @@ def step_probe(args):
 
     torch.cuda.init()
     lib = bench_lib()
-    for mode, wps, what in ((0, 1, "whole step"), (1, 1, "32 MFMAs alone"),
-                            (2, 1, "softmax VALU work alone"), (0, 2, "whole step, 2 waves per SIMD")):
-        us = ctypes.c_float()
-        rc = lib.cie_bench_step_probe(mode, wps, 2000, ctypes.byref(us))
-        if rc != 0:
-            raise RuntimeError(f"cie_bench_step_probe failed: status {rc}")
-        per_simd = us.value / wps
-        print(json.dumps({"probe": "mixed step math", "what": what, "waves_per_simd": wps,
-                          "us_per_step_per_wave": round(us.value, 4),
-                          "us_per_step_per_simd": round(per_simd, 4)}), flush=True)
+    for cus in (0, 8):  # every CU, then 8 CUs (the chip's clock with little power drawn)
+        for mode, wps, what in ((0, 1, "whole step"), (1, 1, "32 MFMAs alone"),
+                                (2, 1, "softmax VALU work alone"), (0, 2, "whole step, 2 waves per SIMD")):
+            us = ctypes.c_float()
+            rc = lib.cie_bench_step_probe(mode, wps, 2000, cus, ctypes.byref(us))
+            if rc != 0:
+                raise RuntimeError(f"cie_bench_step_probe failed: status {rc}")
+            per_simd = us.value / wps
+            print(json.dumps({"probe": "mixed step math", "what": what, "cus": cus or "all",
+                              "waves_per_simd": wps, "us_per_step_per_wave": round(us.value, 4),
+                              "us_per_step_per_simd": round(per_simd, 4),
+                              # a 16x16x32 MFMA keeps the matrix core busy 16 cycles
+                              "implied_GHz_if_mfma_bound": round(32 * 16 / us.value / 1e3, 2)
+                              if mode == 1 else None}), flush=True)
 
 
 def probe_sweep(args):

@@ -6,7 +6,8 @@
 // step against 4 column tiles (D = 64) — the pipelined stream's segments:
 // exponentials, P.V MFMAs and S MFMAs of the next step, then the reference-
 // max check — on register-resident operands, one workgroup of 4 waves per
-// CU times `waves_per_simd`, and returns the time per step (one wave's).
+// CU times `waves_per_simd` (on all CUs or the first n_cus), and returns the
+// time per step (one wave's).
 // Modes: 0 the whole step; 1 its 32 MFMAs alone; 2 its softmax VALU work
 // alone (FMA, exponential, conversion, row sums).  Comparing 0 with 1 + 2
 // shows how much of a lone wave's MFMA and VALU work overlaps; comparing
@@ -112,12 +113,17 @@ using namespace cie_bench;
 
 // 0 on success (*us_per_step set), -1 for bad arguments, else a hipError_t.
 // Allocates and frees its own small output buffer; synchronizes the device.
-extern "C" int cie_bench_step_probe(int mode, int waves_per_simd, int iters, float* us_per_step) {
-  if (mode < 0 || mode > 2 || waves_per_simd < 1 || waves_per_simd > 2 || iters < 1 || !us_per_step)
+// n_cus: CUs to occupy (0: all), so a run on a few CUs shows the step at the
+// clock the chip keeps when few CUs draw power.
+extern "C" int cie_bench_step_probe(int mode, int waves_per_simd, int iters, int n_cus,
+                                    float* us_per_step) {
+  if (mode < 0 || mode > 2 || waves_per_simd < 1 || waves_per_simd > 2 || iters < 1 || n_cus < 0 ||
+      !us_per_step)
     return -1;
   int dev = 0, n_cu = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (n_cus > 0 && n_cus < n_cu) n_cu = n_cus;
   const int blocks = n_cu * waves_per_simd;
   float* out = nullptr;
   hipError_t e = hipMalloc(&out, (size_t)blocks * 256 * sizeof(float));
