@@ -324,6 +324,33 @@ def test_rope_matches_transformers_apply_rotary_pos_emb(seed):
     assert torch.equal(ref.rope(x, cos, sin), want)
 
 
+def test_rope_matches_the_compiled_reference_step():
+    """What the reference's compiled step stores: transformers' apply_rotary_pos_emb
+    on fp16 q / k / cos / sin, compiled by torch.compile's inductor (here its CPU
+    code generation, which like its GPU code generation computes an fp16 pointwise
+    chain in fp32 and rounds once at the store), equals the oracle's rope bit for
+    bit — and differs from the same function run eagerly in fp16, which rounds
+    after every operation."""
+    import torch._dynamo
+    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+
+    x, cos, sin = _rope_inputs(4, T=16, H=4)
+    q = x.permute(1, 0, 2)[None].contiguous()  # (batch, heads, T, D), fp16
+    c, s = cos[None], sin[None]
+
+    def step(q, k, c, s):
+        return apply_rotary_pos_emb(q, k, c, s, unsqueeze_dim=1)
+
+    torch._dynamo.reset()
+    qc, kc = torch.compile(step, backend="inductor", fullgraph=True)(q, q, c, s)
+    torch._dynamo.reset()
+    want = ref.rope(x, cos, sin)
+    assert torch.equal(qc[0].permute(1, 0, 2), want)
+    assert torch.equal(kc[0].permute(1, 0, 2), want)
+    qe, _ = step(q, q, c, s)  # eager fp16
+    assert not torch.equal(qe[0].permute(1, 0, 2), want)
+
+
 def test_rope_identity_at_angle_zero_and_rotation_closed_form():
     x, _, _ = _rope_inputs(2)
     T, H, D = x.shape
