@@ -416,7 +416,7 @@ def trace_mixed(args):
             r = t[g, i].tolist()
             info = r[5]
             items.append(dict(g=g, item=i, start=us(r[0]), lookup=us(r[1]), q=us(r[9]), loop=us(r[8]),
-                              wave_loops=[us(x) if x else None for x in r[10:14]],
+                              wave_loops=[us(x) if x else None for x in r[10:14]], wg=r[14],
                               fold=us(r[2]), end=us(r[3]), merge=us(r[4]) if r[4] else None,
                               nct=info // 1000000, nch=(info // 10000) % 100, ktiles=info % 10000,
                               seq=r[7] // 1000, qt=r[7] % 1000))

@@ -126,7 +126,13 @@ struct TileLaneOffsets {
         v((uint32_t)((4 * grp * D + Geo<D>::NT * r16) * sizeof(f16))) {}
 };
 
-template <int D>
+// Cache-policy operand of a raw buffer load: nt (non-temporal, not kept for
+// reuse).
+constexpr int kBufNt = 2;
+
+// VPOL: cache policy of the V loads (kBufNt for rows read once: a stream
+// that no other work item reads again).
+template <int D, int VPOL = 0>
 __device__ __forceinline__ void load_tile_buf(f16x8 (&k)[Geo<D>::KS],
                                               typename HVec<Geo<D>::NT>::type (&v)[4],
                                               __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
@@ -140,9 +146,9 @@ __device__ __forceinline__ void load_tile_buf(f16x8 (&k)[Geo<D>::KS],
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     if constexpr (NT == 4)
-      v[e] = __builtin_bit_cast(vrow_t, __builtin_amdgcn_raw_buffer_load_b64(rv, lo.v + e * D * 2, 0, 0));
+      v[e] = __builtin_bit_cast(vrow_t, __builtin_amdgcn_raw_buffer_load_b64(rv, lo.v + e * D * 2, 0, VPOL));
     else
-      v[e] = __builtin_bit_cast(vrow_t, __builtin_amdgcn_raw_buffer_load_b128(rv, lo.v + e * D * 2, 0, 0));
+      v[e] = __builtin_bit_cast(vrow_t, __builtin_amdgcn_raw_buffer_load_b128(rv, lo.v + e * D * 2, 0, VPOL));
   }
 }
 
@@ -387,7 +393,7 @@ __device__ __forceinline__ int lane_page_id(const PagedSrc& src, int c0, int t_e
 // any K/V load (or at once when the wave has no tiles): the caller stages
 // operands there (its Q), so their loads and the page ids' take one memory
 // round trip together.
-template <int D, int NCT, int PF, class QS, class Prologue>
+template <int D, int NCT, int PF, class QS, class Prologue, int VPOL = 0>
 __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& qop,
                                              const int (&lim)[NCT], int t_begin, int t_end,
                                              int key_end, const PagedSrc& src, float scale_log2,
@@ -444,10 +450,12 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
       const int64_t ob = two ? readlane64(toff, ka + 1) : oa;
       typedef typename HVec<Geo<D>::NT>::type vrow_t;
       typedef vrow_t vquad_t[4];
-      load_tile_buf<D>(ring[slot].k[0], *reinterpret_cast<vquad_t*>(&ring[slot].v[0]),
-                       tile_rsrc<D>(src.k_pool, oa, rows_a), tile_rsrc<D>(src.v_pool, oa, rows_a), lanes);
-      load_tile_buf<D>(ring[slot].k[1], *reinterpret_cast<vquad_t*>(&ring[slot].v[4]),
-                       tile_rsrc<D>(src.k_pool, ob, rows_b), tile_rsrc<D>(src.v_pool, ob, rows_b), lanes);
+      load_tile_buf<D, VPOL>(ring[slot].k[0], *reinterpret_cast<vquad_t*>(&ring[slot].v[0]),
+                             tile_rsrc<D>(src.k_pool, oa, rows_a), tile_rsrc<D>(src.v_pool, oa, rows_a),
+                             lanes);
+      load_tile_buf<D, VPOL>(ring[slot].k[1], *reinterpret_cast<vquad_t*>(&ring[slot].v[4]),
+                             tile_rsrc<D>(src.k_pool, ob, rows_b), tile_rsrc<D>(src.v_pool, ob, rows_b),
+                             lanes);
       keya[slot] = key0a;
       keyb[slot] = two ? key0a + 16 : kNoKey;
     };

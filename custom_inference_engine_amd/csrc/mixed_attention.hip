@@ -20,8 +20,8 @@
 // split over the workgroup's waves; every wave carries all of the group's
 // column tiles, so each K/V byte is loaded once per workgroup and reused by
 // every column of the group in registers.  The waves fold their states
-// through LDS one column tile at a time.  A single-chunk item writes o
-// directly.  Otherwise each chunk writes its partial (m, l, acc) per column
+// through LDS in one round (wave c combines column tile c).  A single-chunk
+// item writes o directly.  Otherwise each chunk writes its partial (m, l, acc) per column
 // with device-coherent stores and the last chunk to arrive (counter per
 // tile and column group) merges them with log-sum-exp, writes o and resets
 // the counter.  The reference instead walks a tile's whole prefix with one
@@ -69,11 +69,19 @@ namespace cie {
 #ifndef CIE_MIXED_NARROW_PAIRS
 #define CIE_MIXED_NARROW_PAIRS 8
 #endif
+#ifndef CIE_MIXED_NARROW_PF
+#define CIE_MIXED_NARROW_PF 1
+#endif
+#ifndef CIE_MIXED_NARROW_NT
+#define CIE_MIXED_NARROW_NT 1
+#endif
+#ifndef CIE_MIXED_NARROW_ORDER
+#define CIE_MIXED_NARROW_ORDER 0
+#endif
 
 constexpr int kWavePairs = CIE_MIXED_WAVE_PAIRS;
 constexpr int kMaxChunks = 16;    // workgroups per (tile, column group) at most
 constexpr int kMaxColGroups = 8;  // column groups per tile at most (<= 8 column tiles)
-constexpr int kFoldTiles = 2;     // column tiles whose wave states share one fold round
 
 
 // Wavefronts per workgroup, column tiles per work item (registers: 16*NT
@@ -98,11 +106,18 @@ template <int D>
 constexpr int mixed_pf() {
   return D <= 64 ? CIE_MIXED_PF : 1;
 }
+// The same for a work item of one column tile (a decode row): its steps are
+// short, so more of them are kept in flight.
+template <int D, int NCT>
+constexpr int stream_pf() {
+  return D <= 64 && NCT == 1 ? CIE_MIXED_NARROW_PF : mixed_pf<D>();
+}
 
-// Column tiles of one fold round at head dim D (a group may have fewer).
-template <int D>
-constexpr int fold_tiles() {
-  return col_group<D>() < kFoldTiles ? col_group<D>() : kFoldTiles;
+// LDS slot of wave w's state of column tile c in the fold (wave c folds
+// column tile c and keeps its own state in registers: W - 1 slots a tile).
+template <int W>
+__device__ __forceinline__ int fold_slot(int w, int c) {
+  return c * (W - 1) + (w < c ? w : w - 1);
 }
 
 struct MixedParams {
@@ -244,14 +259,14 @@ __shared__ uint64_t sm_mixed_trace[16];
   do {                                                                                 \
     if ((threadIdx.x & (kWave - 1)) == 0) sm_mixed_trace[(k) + threadIdx.x / kWave] = (v); \
   } while (0)
-#define MIXED_TRACE_FLUSH(item)                                                              \
-  do {                                                                                       \
-    if (threadIdx.x == 0 && g_mixed_trace != nullptr && (item) < 4096) {                     \
-      for (int k_ = 0; k_ < 16; ++k_)                                                        \
-        g_mixed_trace[((int64_t)blockIdx.y * 4096 + (item)) * 16 + k_] = sm_mixed_trace[k_]; \
-      for (int k_ = 0; k_ < 16; ++k_)                                                        \
-        if (k_ != 6) sm_mixed_trace[k_] = 0;                                                 \
-    }                                                                                        \
+#define MIXED_TRACE_FLUSH(head, item)                                                   \
+  do {                                                                                  \
+    if (threadIdx.x == 0 && g_mixed_trace != nullptr && (item) < 4096) {                \
+      for (int k_ = 0; k_ < 16; ++k_)                                                   \
+        g_mixed_trace[((int64_t)(head) * 4096 + (item)) * 16 + k_] = sm_mixed_trace[k_]; \
+      for (int k_ = 0; k_ < 16; ++k_)                                                   \
+        if (k_ != 6 && k_ != 14) sm_mixed_trace[k_] = 0;                                \
+    }                                                                                   \
   } while (0)
 #else
 #define MIXED_TRACE(item, k, v) \
@@ -260,8 +275,8 @@ __shared__ uint64_t sm_mixed_trace[16];
 #define MIXED_TRACE_WAVE(k, v) \
   do {                         \
   } while (0)
-#define MIXED_TRACE_FLUSH(item) \
-  do {                          \
+#define MIXED_TRACE_FLUSH(head, item) \
+  do {                                \
   } while (0)
 #endif
 
@@ -333,8 +348,9 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
       stream_tiles_pipelined<D, NCT>(st, QLds<D>{sm_q, lane}, lims, w0, w1, tp.key_end, src,
                                      p.scale_log2, r16, grp, stage_q);
     else
-      stream_tiles<D, NCT, mixed_pf<D>()>(st, QLds<D>{sm_q, lane}, lim, w0, w1, tp.key_end, src,
-                                          p.scale_log2, r16, grp, stage_q);
+      stream_tiles<D, NCT, stream_pf<D, NCT>(), QLds<D>, decltype(stage_q),
+                   NCT == 1 && CIE_MIXED_NARROW_NT ? kBufNt : 0>(
+          st, QLds<D>{sm_q, lane}, lim, w0, w1, tp.key_end, src, p.scale_log2, r16, grp, stage_q);
   } else {
     f16x8 qop[NCT][KS];
     int lim[NCT];
@@ -346,17 +362,15 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
   }
   MIXED_TRACE(item, 8, __builtin_amdgcn_s_memrealtime());
   MIXED_TRACE_WAVE(10, __builtin_amdgcn_s_memrealtime());
-  // Fold the waves' states, kFoldTiles column tiles per round: every wave
-  // puts its states of the round's column tiles into LDS in its register
-  // layout, and after a barrier wave c combines column tile c lane by lane —
-  // each lane reads its own (column, dims) slots of the other waves' states,
-  // so the reads are conflict-free and the SIMDs fold their tiles at once —
-  // and writes o (single chunk) or the chunk's partial.  (Every column tile
-  // in one round needs 72 KB of LDS at D = 64; past ~72 KB per workgroup the
-  // kernel's loads slow down, measured: unused LDS up to 72 KB cost nothing,
-  // 109 KB cost 12 %.)
+  // Fold the waves' states in one round: every wave puts its states of the
+  // other waves' column tiles into LDS in its register layout (one slot per
+  // (wave, column tile), fold_slot), and after one barrier wave c combines
+  // column tile c lane by lane — each lane reads its own (column, dims) slots
+  // of the other waves' states, so the reads are conflict-free and the SIMDs
+  // fold their tiles at once — and writes o (single chunk) or the chunk's
+  // partial.  Nothing waits for the fold to end: the next item's first LDS
+  // writes (its Q) touch no slot, and its own fold follows its Q barrier.
   static_assert(NCT <= W, "a wave per column tile of the group");
-  constexpr int FT = fold_tiles<D>();
   // lane ids derived afresh: nothing lane-dependent of the fold is held in
   // registers through the key loop
   const int lane = opaque((int)threadIdx.x) & (kWave - 1);
@@ -365,19 +379,17 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
   const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
   const PartRegion pr = part_region<D>(p, s, tp);
 #pragma unroll
-  for (int c0 = 0; c0 < NCT; c0 += FT) {
-    if (c0 > 0) __syncthreads();  // the previous round's reads are done
+  for (int c = 0; c < NCT; ++c) {
+    if (c == wave) continue;  // wave c keeps its own state in registers
+    const int slot = fold_slot<W>(wave, c);
 #pragma unroll
-    for (int c = c0; c < NCT && c < c0 + FT; ++c) {
-      if (c == wave) continue;  // wave c keeps its own state in registers
+    for (int nt = 0; nt < NT; ++nt) sm_facc[(slot * NT + nt) * kWave + lane] = st.acc[c][nt];
+    sm_fml[slot * kWave + lane] = float2{st.m[c], st.l(c)};
+  }
+  __syncthreads();
+  {
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        sm_facc[((wave * FT + c - c0) * NT + nt) * kWave + lane] = st.acc[c][nt];
-      sm_fml[(wave * FT + c - c0) * kWave + lane] = float2{st.m[c], st.l(c)};
-    }
-    __syncthreads();
-#pragma unroll
-    for (int c = c0; c < NCT && c < c0 + FT; ++c) {
+    for (int c = 0; c < NCT; ++c) {
       if (c != wave) continue;
       float mw[W], lw[W];
 #pragma unroll
@@ -386,7 +398,7 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
           mw[w] = st.m[c];
           lw[w] = st.l(c);
         } else {
-          const float2 ml = sm_fml[(w * FT + c - c0) * kWave + lane];
+          const float2 ml = sm_fml[fold_slot<W>(w, c) * kWave + lane];
           mw[w] = ml.x;
           lw[w] = ml.y;
         }
@@ -407,7 +419,7 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
           num[nt] += a * (w == c ? st.acc[c][nt]
-                                 : sm_facc[((w * FT + c - c0) * NT + nt) * kWave + lane]);
+                                 : sm_facc[(fold_slot<W>(w, c) * NT + nt) * kWave + lane]);
       }
       const int n_cols = min(16, tp.n_combos - (ct0 + c) * 16);
       if (r16 < n_cols) {
@@ -447,80 +459,230 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
 }
 
 // Last chunk of a (tile, column group): combine the n_chunks partials of the
-// group's columns into o.  A thread takes 4 consecutive dims of one column
+// group's columns into o.  A unit is 4 consecutive dims of one column
 // (consecutive threads: consecutive dims, so every load is a whole-line
-// 16-byte access) and walks the chunks in groups of four with a running
-// log-sum-exp, so each group's loads go out together.
+// 16-byte access); a thread holds up to kUnits units and, per group of four
+// chunks, issues the loads of all of them before combining any, so a merge
+// of up to four chunks is one memory round trip; chunks are combined with a
+// running log-sum-exp.
 template <int D>
 __device__ __forceinline__ void merge_group(const MixedParams& p, const SeqInfo& s,
                                             const TilePlan& tp, int g, int ct0, int n_cols) {
   constexpr int kGroup = 4;
+  constexpr int NTH = mixed_waves<D>() * kWave;
+  constexpr int kUnits = (16 * col_group<D>() * (D / 4) + NTH - 1) / NTH;
   const int K = tp.n_chunks;
+  const int n_units = n_cols * (D / 4);
   const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
   const PartRegion pr = part_region<D>(p, s, tp);
-  for (int it = opaque((int)threadIdx.x); it < n_cols * (D / 4); it += mixed_waves<D>() * kWave) {
-    const int j = it / (D / 4);
-    const int d = (it - j * (D / 4)) * 4;
-    const int off = column_off(p, g, ct0 * 16 + j);
-    float M = kNegInf, den = 0.f;
-    f32x4 num = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < K; k0 += kGroup) {
-      float mk[kGroup], lk[kGroup];
-      f32x4 val[kGroup];
+  const int tid = opaque((int)threadIdx.x);
+  int off[kUnits], d4[kUnits];
+  bool live[kUnits];
+  float M[kUnits], den[kUnits];
+  f32x4 num[kUnits];
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
-        const int prow = off * kMaxChunks + k0 + u;
-        if (k0 + u < K) {
-          mk[u] = agent_load(pr.m + prow);
-          lk[u] = agent_load(pr.l + prow);
-          val[u] = agent_load4(pr.acc, (uint32_t)((prow * D + d) * sizeof(float)));
+  for (int u = 0; u < kUnits; ++u) {
+    const int it = tid + u * NTH;
+    live[u] = it < n_units;
+    const int j = live[u] ? it / (D / 4) : 0;
+    d4[u] = (it - j * (D / 4)) * 4;
+    off[u] = column_off(p, g, ct0 * 16 + j);
+    M[u] = kNegInf;
+    den[u] = 0.f;
+    num[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int k0 = 0; k0 < K; k0 += kGroup) {
+    float mk[kUnits][kGroup], lk[kUnits][kGroup];
+    f32x4 val[kUnits][kGroup];
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u)
+#pragma unroll
+      for (int c = 0; c < kGroup; ++c) {
+        const int prow = off[u] * kMaxChunks + k0 + c;
+        if (live[u] && k0 + c < K) {
+          mk[u][c] = agent_load(pr.m + prow);
+          lk[u][c] = agent_load(pr.l + prow);
+          val[u][c] = agent_load4(pr.acc, (uint32_t)((prow * D + d4[u]) * sizeof(float)));
         } else {
-          mk[u] = kNegInf;
-          lk[u] = 0.f;
-          val[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+          mk[u][c] = kNegInf;
+          lk[u][c] = 0.f;
+          val[u][c] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
       }
-      float Mg = M;
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) Mg = fmaxf(Mg, mk[u]);
+    for (int u = 0; u < kUnits; ++u) {
+      float Mg = M[u];
+#pragma unroll
+      for (int c = 0; c < kGroup; ++c) Mg = fmaxf(Mg, mk[u][c]);
       if (Mg == kNegInf) continue;  // nothing attended so far
-      const float rs = fast_exp2(M - Mg);  // 0 when M = -inf
-      den *= rs;
-      num *= rs;
+      const float rs = fast_exp2(M[u] - Mg);  // 0 when M = -inf
+      den[u] *= rs;
+      num[u] *= rs;
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
-        const float a = mk[u] == kNegInf ? 0.f : fast_exp2(mk[u] - Mg);
-        den = __builtin_fmaf(a, lk[u], den);
-        num += a * val[u];
+      for (int c = 0; c < kGroup; ++c) {
+        const float a = mk[u][c] == kNegInf ? 0.f : fast_exp2(mk[u][c] - Mg);
+        den[u] = __builtin_fmaf(a, lk[u][c], den[u]);
+        num[u] += a * val[u][c];
       }
-      M = Mg;
+      M[u] = Mg;
     }
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    const f16x4 h = {(f16)(num[0] * inv), (f16)(num[1] * inv), (f16)(num[2] * inv),
-                     (f16)(num[3] * inv)};
-    *reinterpret_cast<f16x4*>(p.o + (tile_row0 + off) * D + d) = h;
+  }
+#pragma unroll
+  for (int u = 0; u < kUnits; ++u) {
+    if (!live[u]) continue;
+    const float inv = den[u] > 0.f ? 1.f / den[u] : 0.f;
+    const f16x4 h = {(f16)(num[u][0] * inv), (f16)(num[u][1] * inv), (f16)(num[u][2] * inv),
+                     (f16)(num[u][3] * inv)};
+    *reinterpret_cast<f16x4*>(p.o + (tile_row0 + off[u]) * D + d4[u]) = h;
   }
 }
 
 constexpr int kMaxSeqs = 1024;  // sequences a launch can plan (LDS plan tables)
+constexpr int kRankSeqs = 64;   // batches up to this size deal their items heaviest first
 
-// Bytes of the kernel's dynamic LDS: the plan tables of B sequences (t0 as
-// int64, slot / rows / prior / item prefix as int32).
+// Bytes of the kernel's dynamic LDS: the plan tables of B sequences — t0 as
+// int64; slot, rows, prior, the order and the item prefix (B + 1 entries)
+// as int32; a weight per sequence when B <= kRankSeqs.
 static size_t mixed_plan_lds(int B) {
-  return (size_t)B * sizeof(int64_t) + (size_t)(4 * B + 1) * sizeof(int);
+  return (size_t)B * sizeof(int64_t) +
+         (size_t)(4 * B + (B + 1) + (B <= kRankSeqs ? B : 0)) * sizeof(int);
 }
 
-// Items of sequence s: sum over its (grid-covered) query tiles of
-// column groups x chunks.
+// A sequence's tiles and their items.  Full (16-row) tiles all have the same
+// column groups and a chunk count that grows with the tile index: with
+// c16 = ceil(prior / 16), full tile t has c16 + t + 1 key tiles and
+// clamp(ceil((c16 + t + 1) / Q), 1, kMaxChunks) chunks for Q key tiles per
+// chunk (tile_plan's rule), so the tiles group into runs of equal chunk
+// count that are counted and searched without walking the tiles.  A
+// sequence's items are walked heaviest first: its partial last tile (if
+// any), then its full tiles from the top down.
+struct SeqTiles {
+  int n_tiles;  // query tiles computed (the grid's max_seqlen cap applied)
+  int n_full;   // full tiles among them
+  int c16;
+  bool partial;  // tile n_tiles - 1 has fewer than 16 rows
+  int ng_full;   // column groups of a full tile
+  bool full_narrow;  // a full tile is one column tile (G = 1): narrow chunks
+};
+
 template <int CG, int W>
-__device__ __forceinline__ int seq_items(const SeqInfo& s, int n_qtiles, int G) {
-  const int n_tiles = min((s.L + 15) >> 4, n_qtiles);
-  int n = 0;
-  for (int qt = 0; qt < n_tiles; ++qt) {
-    const TilePlan tp = tile_plan<CG, W>(qt, s, G);
-    n += tp.n_groups * tp.n_chunks;
+__device__ __forceinline__ SeqTiles seq_tiles(const SeqInfo& s, int n_qtiles, int G) {
+  SeqTiles t;
+  t.n_tiles = min((s.L + 15) >> 4, n_qtiles);
+  t.n_full = min(s.L >> 4, t.n_tiles);
+  t.c16 = (s.c + 15) >> 4;
+  t.partial = t.n_tiles > t.n_full;
+  t.ng_full = (G + CG - 1) / CG;
+  t.full_narrow = G <= 1;
+  return t;
+}
+
+// Visit the runs of full tiles [0, n) with equal chunk counts (Q key tiles a
+// chunk), from the top tile down: f(t_lo, t_hi, k) returns true to stop.
+template <int Q, class F>
+__device__ __forceinline__ void chunk_runs(int n, int c16, F f) {
+  for (int t_hi = n - 1; t_hi >= 0;) {
+    const int k = min(kMaxChunks, (c16 + t_hi + 1 + Q - 1) / Q);
+    // lowest tile with the same (clamped) count: c16 + t + 1 > (k - 1) * Q
+    const int t_lo = k == 1 ? 0 : max(0, (k - 1) * Q - c16);
+    if (f(t_lo, t_hi, k)) return;
+    t_hi = t_lo - 1;
   }
+}
+
+template <int W>
+constexpr int wide_chunk_ktiles() {
+  return 2 * W * kWavePairs;
+}
+template <int W>
+constexpr int narrow_chunk_ktiles() {
+  return 2 * W * CIE_MIXED_NARROW_PAIRS;
+}
+
+template <int W, class F>
+__device__ __forceinline__ void full_runs(const SeqTiles& st, F f) {
+  if (st.full_narrow) chunk_runs<narrow_chunk_ktiles<W>()>(st.n_full, st.c16, f);
+  else chunk_runs<wide_chunk_ktiles<W>()>(st.n_full, st.c16, f);
+}
+
+// Items of one sequence, and its weight: the key tiles of its heaviest
+// chunk (the top tile's), the order in which batches of up to kRankSeqs
+// sequences deal their items.
+template <int CG, int W>
+__device__ __forceinline__ int seq_items(const SeqInfo& s, const SeqTiles& st, int G, int& weight) {
+  int n = 0;
+  weight = 0;
+  if (st.n_tiles <= 0) return 0;
+  const TilePlan top = tile_plan<CG, W>(st.n_tiles - 1, s, G);
+  weight = (top.n_ktiles + top.n_chunks - 1) / top.n_chunks;
+  if (st.n_tiles == 1 && top.n_ctiles == 1) {  // one narrow tile (a decode row)
+    if (CIE_MIXED_NARROW_ORDER == 1) weight = 0;
+    if (CIE_MIXED_NARROW_ORDER == 2) weight += 1 << 24;
+  }
+  if (st.partial) n += top.n_groups * top.n_chunks;
+  const int ng = st.ng_full;
+  full_runs<W>(st, [&](int lo, int hi, int k) {
+    n += (hi - lo + 1) * ng * k;
+    return false;
+  });
   return n;
+}
+
+// Item j of one sequence: its query tile and its index among the tile's
+// items (column group * chunks + chunk).
+template <int CG, int W>
+__device__ __forceinline__ void seq_locate(const SeqInfo& s, const SeqTiles& st, int G, int j,
+                                           int& qt, int& jt) {
+  qt = st.n_tiles - 1;
+  jt = j;
+  if (st.partial) {
+    const TilePlan tp = tile_plan<CG, W>(st.n_tiles - 1, s, G);
+    const int np = tp.n_groups * tp.n_chunks;
+    if (j < np) return;
+    j -= np;
+  }
+  const int ng = st.ng_full;
+  full_runs<W>(st, [&](int lo, int hi, int k) {
+    const int per = ng * k;
+    const int cnt = (hi - lo + 1) * per;
+    if (j < cnt) {
+      const int d = j / per;
+      qt = hi - d;
+      jt = j - d * per;
+      return true;
+    }
+    j -= cnt;
+    return false;
+  });
+}
+
+// Inclusive sum of (x, y) over the workgroup's threads (sm: NTH int2).
+template <int NTH>
+__device__ __forceinline__ int2 block_scan2(int2 v, int2* sm) {
+  sm[threadIdx.x] = v;
+  __syncthreads();
+  for (int off = 1; off < NTH; off <<= 1) {
+    const int2 add = threadIdx.x >= (unsigned)off ? sm[threadIdx.x - off] : int2{0, 0};
+    __syncthreads();
+    v.x += add.x;
+    v.y += add.y;
+    sm[threadIdx.x] = v;
+    __syncthreads();
+  }
+  return v;
+}
+
+// Last index i in [0, n) with prefix[i] <= x (prefix nondecreasing,
+// prefix[0] <= x): i + 1 such entries, counted 64 per LDS read with a ballot.
+__device__ __forceinline__ int prefix_search(const int* prefix, int n, int x) {
+  int n_le = 0;
+  for (int i0 = 0; i0 < n; i0 += kWave) {
+    const int i = i0 + (int)(threadIdx.x & (kWave - 1));
+    const uint64_t le = __ballot(i < n && prefix[i] <= x);
+    n_le += __popcll(le);
+    if (~le != 0) break;
+  }
+  return uniform(n_le - 1);
 }
 
 // One work item: column group gi, chunk `chunk` of query tile qt of sequence
@@ -565,10 +727,11 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   }
   MIXED_TRACE(item, 2, __builtin_amdgcn_s_memrealtime());
   MIXED_TRACE(item, 5, (uint64_t)(tp.n_ctiles * 1000000 + tp.n_chunks * 10000 + (kt1 - kt0)));
+  // (no barrier before the next item: its first LDS writes, the Q copy,
+  // touch nothing the fold reads, and its Q barrier orders the rest)
   if (tp.n_chunks == 1) {
-    __syncthreads();  // LDS is reused by the next item
     MIXED_TRACE(item, 3, __builtin_amdgcn_s_memrealtime());
-    MIXED_TRACE_FLUSH(item);
+    MIXED_TRACE_FLUSH(g, item);
     return;
   }
   // The last chunk of this (tile, column group) to arrive merges all chunks.
@@ -580,15 +743,16 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
     merge_group<D>(p, s, tp, g, ct0, min(16 * n, tp.n_combos - 16 * ct0));
     if (threadIdx.x == 0) counter_reset(ctr);
   }
-  __syncthreads();
   MIXED_TRACE(item, 3, __builtin_amdgcn_s_memrealtime());
-  MIXED_TRACE_FLUSH(item);
+  MIXED_TRACE_FLUSH(g, item);
 }
 
-// Grid (n_workgroups, H_kv): every workgroup plans the whole batch — per
-// sequence item counts and their prefix sums in LDS — and takes items
-// blockIdx.x, blockIdx.x + gridDim.x, ...  (items ordered by sequence, tile,
-// column group, chunk), so no workgroup is launched for an empty slot.
+// Grid: one workgroup per CU, a whole number per kv head (workgroup w serves
+// kv head w % H_kv).  Every workgroup plans the whole batch — per sequence
+// item counts, the order in which sequences deal their items (heaviest
+// first for batches of up to kRankSeqs sequences) and the item prefix by
+// that order, in LDS — and takes its kv head's items round by round
+// (see the item loop), so no workgroup is launched for an empty slot.
 // Waves per SIMD the registers must allow: two when a wave carries at most
 // two column tiles or keeps its Q operands in LDS (D = 64), else one.
 template <int D>
@@ -603,116 +767,128 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
   static_assert(col_group<D>() <= 4 && 8 / col_group<D>() <= kMaxColGroups, "column groups");
   constexpr int W = mixed_waves<D>();
   constexpr int NTH = W * kWave;
-  // the waves' states of a fold round: [wave][column tile][d-tile][lane]
-  // (acc) and [wave][column tile][lane] (m, l)
-  constexpr int kFold = W * fold_tiles<D>();
+  // the waves' states in the fold: [slot][d-tile][lane] (acc) and
+  // [slot][lane] (m, l), slot = fold_slot(wave, column tile)
+  constexpr int kFold = col_group<D>() * (W - 1);
   __shared__ f32x4 sm_facc[kFold * Geo<D>::NT * kWave];
   __shared__ float2 sm_fml[kFold * kWave];
   __shared__ f16x8 sm_q[CIE_MIXED_QLDS ? col_group<D>() * Geo<D>::KS * kWave : 1];
   __shared__ int sm_last;
-  __shared__ int sm_scan[NTH];
-  // The plan, in LDS sized by the launch to the batch (mixed_plan_lds): the
-  // item prefix per sequence and each sequence's seq_info, so an item starts
-  // its Q and page-id loads without reading the sequence tables again.
+  __shared__ int2 sm_scan[NTH];
+  // The plan, in LDS sized by the launch to the batch (mixed_plan_lds): each
+  // sequence's seq_info, so an item starts its Q and page-id loads without
+  // reading the sequence tables again, the order in which sequences deal
+  // their items, and the item prefix by that order.
   extern __shared__ __attribute__((aligned(16))) char sm_plan[];
+  const int B = p.B;
   int64_t* const sm_t0 = reinterpret_cast<int64_t*>(sm_plan);
-  int* const sm_slot = reinterpret_cast<int*>(sm_t0 + p.B);
-  int* const sm_rows = sm_slot + p.B;
-  int* const sm_prior = sm_rows + p.B;
-  int* const sm_prefix = sm_prior + p.B;  // B + 1 entries
+  int* const sm_slot = reinterpret_cast<int*>(sm_t0 + B);
+  int* const sm_rows = sm_slot + B;
+  int* const sm_prior = sm_rows + B;
+  int* const sm_order = sm_prior + B;    // position -> sequence
+  int* const sm_prefix = sm_order + B;   // B + 1 entries, by position
+  int* const sm_key = sm_prefix + B + 1;  // B <= kRankSeqs: weight per sequence
 
   constexpr int CG = col_group<D>();
-  const int g = blockIdx.y;
-  // Per-thread item counts of sequences b = tid, tid + NTH, ... (B <= kMaxSeqs).
-  int base = 0;
-  for (int b0 = 0; b0 < p.B; b0 += NTH) {
-    const int b = b0 + threadIdx.x;
-    int n = 0;
-    if (b < p.B) {
-      const SeqInfo s = seq_info(p, b);
-      sm_t0[b] = s.t0;
-      sm_slot[b] = (int)s.slot;
-      sm_rows[b] = s.L;
-      sm_prior[b] = s.c;
-      if (g == 0 && blockIdx.x == 0 && ((s.L + 15) >> 4) > p.n_qtiles)
-        set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
-      n = s.L > 0 ? seq_items<CG, W>(s, p.n_qtiles, p.G) : 0;
+  // Pass 1, sequences b = tid, tid + NTH, ... (B <= kMaxSeqs): tables and
+  // each sequence's item count (parked in sm_prefix[b + 1] until the order
+  // is known) and weight.
+  const bool rank = B <= kRankSeqs;
+  for (int b = threadIdx.x; b < B; b += NTH) {
+    const SeqInfo s = seq_info(p, b);
+    sm_t0[b] = s.t0;
+    sm_slot[b] = (int)s.slot;
+    sm_rows[b] = s.L;
+    sm_prior[b] = s.c;
+    if (blockIdx.x == 0 && ((s.L + 15) >> 4) > p.n_qtiles)
+      set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
+    int n = 0, weight = 0;
+    if (s.L > 0) n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, weight);
+    sm_prefix[b + 1] = n;
+    if (rank) sm_key[b] = n > 0 ? weight : -1;
+  }
+  __syncthreads();
+  // Order: heaviest sequence first (B <= kRankSeqs; ties by b), else by b.
+  if (rank) {
+    int pos = -1, cnt = 0;
+    if ((int)threadIdx.x < B) {
+      const int b = threadIdx.x;
+      const int kb = sm_key[b];
+      cnt = sm_prefix[b + 1];
+      pos = 0;
+      for (int o = 0; o < B; ++o) {
+        const int ko = sm_key[o];
+        pos += (ko > kb || (ko == kb && o < b)) ? 1 : 0;
+      }
     }
-    // inclusive block scan of n over this pass's span of sequences
-    const int span = min(NTH, p.B - b0);
-    sm_scan[threadIdx.x] = n;
     __syncthreads();
-    for (int off = 1; off < span; off <<= 1) {
-      const int add = threadIdx.x >= off ? sm_scan[threadIdx.x - off] : 0;
-      __syncthreads();
-      sm_scan[threadIdx.x] += add;
-      __syncthreads();
+    if (pos >= 0) {
+      sm_order[pos] = threadIdx.x;
+      sm_prefix[pos + 1] = cnt;
     }
-    if (b < p.B) sm_prefix[b + 1] = base + sm_scan[threadIdx.x];
-    base += sm_scan[span - 1];
+  } else {
+    for (int b = threadIdx.x; b < B; b += NTH) sm_order[b] = b;
+  }
+  __syncthreads();
+  // item prefix over positions
+  int base = 0;
+  for (int q0 = 0; q0 < B; q0 += NTH) {
+    const int q = q0 + threadIdx.x;
+    const int c = q < B ? sm_prefix[q + 1] : 0;
+    const int2 inc = block_scan2<NTH>(int2{c, 0}, sm_scan);
+    const int tot = sm_scan[NTH - 1].x;
+    if (q < B) sm_prefix[q + 1] = base + inc.x;
+    base += tot;
     __syncthreads();
   }
   if (threadIdx.x == 0) sm_prefix[0] = 0;
   __syncthreads();
-  // (LDS reads look per-lane to the compiler: the plan's values are pinned
-  // to scalar registers, so everything derived from them stays scalar)
-  const int total = uniform(sm_prefix[p.B]);
-  MIXED_TRACE(blockIdx.x, 6, __builtin_amdgcn_s_memrealtime());  // planning done (first item slot)
+  const int n_items = uniform(base);
+  const int g = blockIdx.x % p.H_kv;
+  const int slot_r = blockIdx.x / p.H_kv;
+  const int n_slots_r = gridDim.x / p.H_kv;  // workgroups per kv head
+  MIXED_TRACE(0, 6, __builtin_amdgcn_s_memrealtime());  // planning done
+  MIXED_TRACE(0, 14, (uint64_t)blockIdx.x);
 
-  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+  // Items go to the kv head's workgroups in rounds, alternating direction
+  // (round q, position w: item q * n + (q even ? w : n - 1 - w)), so the
+  // workgroups that took the heaviest items of round 0 take the lightest of
+  // round 1.
+  for (int q = 0; slot_r < n_slots_r; ++q) {
+    const int item = q * n_slots_r + ((q & 1) ? n_slots_r - 1 - slot_r : slot_r);
+    if (item >= n_items) break;
     MIXED_TRACE(item, 0, __builtin_amdgcn_s_memrealtime());
-    // sequence: last b with prefix[b] <= item (binary search)
-    int lo = 0, hi = p.B;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (uniform(sm_prefix[mid]) <= item) lo = mid;
-      else hi = mid;
-    }
-    const int b = uniform(lo);
+    const int pos = prefix_search(sm_prefix, B, item);
+    const int b = uniform(sm_order[pos]);
+    const int j = item - uniform(sm_prefix[pos]);
     SeqInfo s;
     s.t0 = uniform64(sm_t0[b]);
     s.slot = uniform(sm_slot[b]);
     s.L = uniform(sm_rows[b]);
     s.c = uniform(sm_prior[b]);
-    int j = item - uniform(sm_prefix[b]);
-    int qt = 0;
-    // Full (16-row) tiles all have the same column groups, and their chunk
-    // count grows with the tile index; if the last full tile is one chunk,
-    // every full tile is n_groups items and the item's tile is a division.
-    // Otherwise (and for the partial last tile) walk the tiles.
-    const int n_full = min(s.L >> 4, p.n_qtiles);
-    if (n_full > 0) {
-      const TilePlan lf = tile_plan<CG, W>(n_full - 1, s, p.G);
-      if (lf.n_chunks == 1) {
-        qt = min(j / lf.n_groups, n_full);
-        j -= qt * lf.n_groups;
-      }
-    }
-    for (;; ++qt) {
-      const TilePlan tp = tile_plan<CG, W>(qt, s, p.G);
-      const int nt = tp.n_groups * tp.n_chunks;
-      if (j < nt) break;
-      j -= nt;
-    }
+    int qt, jt;
+    seq_locate<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, j, qt, jt);
     MIXED_TRACE(item, 1, __builtin_amdgcn_s_memrealtime());
     MIXED_TRACE(item, 7, (uint64_t)(b * 1000 + qt));
-    process_item<D, P32>(p, s, b, g, uniform(qt), uniform(j), sm_facc, sm_fml, sm_q, &sm_last,
+    process_item<D, P32>(p, s, b, g, uniform(qt), uniform(jt), sm_facc, sm_fml, sm_q, &sm_last,
                          item);
   }
 }
 
-// Workgroups of the mixed grid: CIE_MIXED_WG_PER_CU per CU over the kv heads.
+// Workgroups of the mixed grid: CIE_MIXED_WG_PER_CU per CU, a whole number
+// per kv head.
 static int mixed_workgroups(int H_kv) {
   int dev = 0, n_cu = 256;
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
-  const int n = n_cu * CIE_MIXED_WG_PER_CU / H_kv;
-  return n > 1 ? n : 1;
+  int per_head = n_cu * CIE_MIXED_WG_PER_CU / H_kv;
+  if (per_head < 1) per_head = 1;
+  return per_head * H_kv;
 }
 
 template <int D>
 static int launch_mixed(const MixedParams& p, hipStream_t stream) {
-  dim3 grid(mixed_workgroups(p.H_kv), p.H_kv, 1);
+  dim3 grid(mixed_workgroups(p.H_kv), 1, 1);
   if (p.pool_bytes != 0)
     hipLaunchKernelGGL((mixed_attention_kernel<D, true>), grid, dim3(mixed_waves<D>() * kWave),
                        mixed_plan_lds(p.B), stream, p);
