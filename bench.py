@@ -76,6 +76,9 @@ def parse():
                     help="with --trace-mixed: also write every item's stamps to PATH as JSON")
     ap.add_argument("--mixed-part", choices=("all", "prefill", "decode"), default="all",
                     help="config 3: time only its prefill chunks or only its decode rows")
+    ap.add_argument("--step-modules", action="store_true",
+                    help="config 5's model: one mixed step (8 sequences x 64 new tokens over 512 cached, "
+                         "token bucket 512) through the eager, full-graph and piecewise step modules")
     return ap.parse_args()
 
 
@@ -542,6 +545,8 @@ def main():
     torch.cuda.set_device(dev)
     if args.config == 3:
         return bench_mixed(args, cie, inputs, ref, dev)
+    if args.step_modules:
+        return bench_step_modules(args, cie, dev)
     if args.config == 5:
         return bench_model(args, cie, dev)
     if args.config == 6:
@@ -967,6 +972,77 @@ def bench_model(args, cie, dev, n_requests: int = 64, n_slots: int = 33, new_tok
                    "prompt_len_sigma": sigma, "prompt_tokens": n_prompt, "new_tokens": new_tokens,
                    "token_budget": budget, "pool_tokens": 32768},
     }
+    print(json.dumps(line), flush=True)
+
+
+def bench_step_modules(args, cie, dev, n_seqs: int = 8, new_tokens: int = 64, prior: int = 512,
+                       bucket: int = 512, steps: int = 20, warmup: int = 3):
+    """One mixed step of config 5's 24-layer model through each step module.
+
+    8 sequences of 64 new tokens over 512 cached ones in the 512-token bucket
+    (`MixedModule` eager, `FullMixedModule` one hipGraph, `PiecewiseMixedModule`
+    graph pieces between eager attention calls).  A step = host upload + the
+    step, ended by a device sync; the cached lengths are set back to `prior`
+    before each step (one small device write, in every mode), so every step
+    does the same work.  Random fp16 weights; ms per step, mean of `steps`."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    from custom_inference_engine_amd.scheduler import (FullMixedModule, MixedModule, PiecewiseMixedModule,
+                                                       assign_pages)
+
+    cfg = Qwen2Config(hidden_size=896, num_attention_heads=14, num_key_value_heads=2, intermediate_size=4864,
+                      num_hidden_layers=24, vocab_size=151936, max_position_embeddings=32768, rope_theta=1e6,
+                      rms_norm_eps=1e-6, tie_word_embeddings=True)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Qwen2ForCausalLM(cfg)
+    model = model.half().eval()
+    cie.use_triton_attention(model)
+    out = {}
+    for kind in ("eager", "full_graph", "piecewise"):
+        torch._dynamo.reset()
+        kv = cie.KVStorage(cfg, max_cache_len=16384, page_size=16, n_slots=33, device=dev, dtype=torch.float16)
+        pool = torch.cuda.graph_pool_handle()
+        t0 = time.perf_counter()
+        if kind == "eager":
+            mod = MixedModule(model, kv, token_count=bucket)
+        elif kind == "full_graph":
+            mod = FullMixedModule(model, kv, batch_size=kv.n_slots - 1, token_count=bucket, pool=pool)
+        else:
+            buf = torch.zeros((1, bucket, cfg.num_attention_heads, 64), dtype=torch.float16, device=dev)
+            mod = PiecewiseMixedModule(model, kv, token_count=bucket, buffer=buf, pool=pool)
+        build_s = time.perf_counter() - t0
+        free = list(range(1, kv.n_pages))
+        slots = list(range(1, n_seqs + 1))
+        for sl in slots:
+            assign_pages(kv, sl, prior + new_tokens, free)
+        slot_t = torch.tensor(slots, device=dev)
+        prompts = [[5] * new_tokens for _ in slots]
+
+        def step():
+            kv.lens[slot_t] = prior
+            mod.upload(prompts, slots)
+            return mod.run()
+
+        with torch.inference_mode():
+            for _ in range(warmup):
+                step()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) / steps * 1e3
+        out[kind] = {"ms_per_step": round(ms, 3), "build_s": round(build_s, 2)}
+        log(f"{kind}: {ms:.3f} ms per step (module built in {build_s:.1f} s)")
+        del mod, kv
+        torch.cuda.empty_cache()
+    line = {"metric": "config 5 model: mixed step ms by step module (diagnostic, not a bench line)",
+            "unit": "ms/step", "higher_is_better": False, "modules": out,
+            "dtype": "fp16 (fp32 accumulate)", "data": "synthetic (random weights, constant token ids)",
+            "config": {"workload": "24-layer Qwen2.5-0.5B shape, one mixed step", "sequences": n_seqs,
+                       "new_tokens": new_tokens, "cached_tokens": prior, "token_bucket": bucket,
+                       "steps": steps}}
     print(json.dumps(line), flush=True)
 
 
