@@ -68,8 +68,9 @@ def parse():
                          "(python -m custom_inference_engine_amd._build -D CIE_DECODE_TRACE --out DIR, "
                          "then CIE_PAGED_LIB=DIR/libcie_paged.so)")
     ap.add_argument("--trace-mixed", action="store_true",
-                    help="per-item phase trace of one config-3 mixed launch; needs a trace build "
-                         "(-D CIE_MIXED_TRACE, loaded through CIE_PAGED_LIB)")
+                    help="per-item phase trace of one config-3 mixed launch (--config 6: the feature "
+                         "bench's B = 1 shape); needs a trace build (-D CIE_MIXED_TRACE, loaded through "
+                         "CIE_PAGED_LIB)")
     ap.add_argument("--step-probe", action="store_true",
                     help="time the mixed kernel's step math alone (MFMA / VALU split, 1 and 2 waves per SIMD)")
     ap.add_argument("--trace-out", default=None, metavar="PATH",
@@ -388,7 +389,10 @@ def trace_mixed(args):
     lib.cie_mixed_trace_buffer.argtypes = [ctypes.c_void_p]
     dev = torch.device("cuda:0")
     case = inputs.config3(seed=0)
-    if args.mixed_part != "all":
+    max_seqlen = 256
+    if args.config == 6:  # the feature bench's B = 1 shape: 128 rows on 256 cached tokens
+        case, max_seqlen = inputs.make_case([256], [128], seed=1), 128
+    elif args.mixed_part != "all":
         prior, new = case.kv_lens.tolist(), case.new_lens.tolist()
         keep = [i for i, n in enumerate(new) if (n > 1) == (args.mixed_part == "prefill")]
         case = inputs.make_case([prior[i] for i in keep], [new[i] for i in keep], seed=0)
@@ -401,7 +405,7 @@ def trace_mixed(args):
     for it in range(3 * R):
         kp, vp = pools[it % R]
         buf.zero_()
-        cie.mixed_gqa_attention(c.q, kp, vp, 256, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table)
+        cie.mixed_gqa_attention(c.q, kp, vp, max_seqlen, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table)
     torch.cuda.synchronize()
     lib.cie_mixed_trace_buffer(None)
     t = buf.view(2, 4096, 16).cpu()
@@ -420,13 +424,16 @@ def trace_mixed(args):
             info = r[5]
             items.append(dict(g=g, item=i, start=us(r[0]), lookup=us(r[1]), q=us(r[9]), loop=us(r[8]),
                               wave_loops=[us(x) if x else None for x in r[10:14]], wg=r[14],
+                              wg_start=us(r[15]) if r[15] else None,
                               fold=us(r[2]), end=us(r[3]), merge=us(r[4]) if r[4] else None,
                               nct=info // 1000000, nch=(info // 10000) % 100, ktiles=info % 10000,
                               seq=r[7] // 1000, qt=r[7] % 1000))
     span = max(x["end"] for x in items)
     crit = max(items, key=lambda x: x["end"])
+    starts = [x["wg_start"] for x in items if x["wg_start"] is not None]
     print(f"items {len(items)}, span {span:.2f} us; planning done (median over workgroups) "
-          f"{statistics.median(us(t[g, i, 6].item()) for g in range(2) for i in range(4096) if t[g, i, 6]):.2f} us")
+          f"{statistics.median(us(t[g, i, 6].item()) for g in range(2) for i in range(4096) if t[g, i, 6]):.2f} us; "
+          f"workgroup starts {min(starts):.2f} .. {max(starts):.2f} us (median {statistics.median(starts):.2f})")
     print("critical item: " + ", ".join(f"{k} {v:.2f}" if isinstance(v, float) else f"{k} {v}"
                                         for k, v in crit.items()))
     print(f"{'class':18s} {'n':>4s} {'start':>6s} {'lookup':>7s} {'Q':>6s} {'loop':>7s} {'fold':>6s} "

@@ -199,10 +199,13 @@ __device__ __forceinline__ TilePlan tile_plan(int qt, const SeqInfo& s, int G) {
 
 // Key tiles [*t0, *t1) of part i of n when a tile's 32-key steps are split
 // into n near-equal runs (run boundaries on whole steps).
+// (32-bit arithmetic: a tile has fewer than 2^27 key tiles — the launch
+// rejects block tables of 2^31 keys — and i < n <= kMaxChunks, so
+// steps * (i + 1) < 2^31)
 __device__ __forceinline__ void split_steps(int t_begin, int t_end, int i, int n, int& t0, int& t1) {
-  const int steps = (t_end - t_begin + 1) >> 1;
-  t0 = min(t_end, t_begin + 2 * (int)((int64_t)steps * i / n));
-  t1 = min(t_end, t_begin + 2 * (int)((int64_t)steps * (i + 1) / n));
+  const uint32_t steps = (uint32_t)(t_end - t_begin + 1) >> 1;
+  t0 = min(t_end, t_begin + 2 * (int)(steps * (uint32_t)i / (uint32_t)n));
+  t1 = min(t_end, t_begin + 2 * (int)(steps * (uint32_t)(i + 1) / (uint32_t)n));
 }
 
 // Q^T operand and key limit of column tile ct (columns = (row, head) pairs).
@@ -265,7 +268,7 @@ __shared__ uint64_t sm_mixed_trace[16];
       for (int k_ = 0; k_ < 16; ++k_)                                                   \
         g_mixed_trace[((int64_t)(head) * 4096 + (item)) * 16 + k_] = sm_mixed_trace[k_]; \
       for (int k_ = 0; k_ < 16; ++k_)                                                   \
-        if (k_ != 6 && k_ != 14) sm_mixed_trace[k_] = 0;                                \
+        if (k_ != 6 && k_ != 14 && k_ != 15) sm_mixed_trace[k_] = 0;                   \
     }                                                                                   \
   } while (0)
 #else
@@ -539,13 +542,13 @@ __device__ __forceinline__ void merge_group(const MixedParams& p, const SeqInfo&
 
 constexpr int kMaxSeqs = 1024;  // sequences a launch can plan (LDS plan tables)
 constexpr int kRankSeqs = 64;   // batches up to this size deal their items heaviest first
+static_assert(kRankSeqs == kWave, "a batch small enough to rank is planned by one wave");
 
 // Bytes of the kernel's dynamic LDS: the plan tables of B sequences — t0 as
 // int64; slot, rows, prior, the order and the item prefix (B + 1 entries)
-// as int32; a weight per sequence when B <= kRankSeqs.
+// as int32.
 static size_t mixed_plan_lds(int B) {
-  return (size_t)B * sizeof(int64_t) +
-         (size_t)(4 * B + (B + 1) + (B <= kRankSeqs ? B : 0)) * sizeof(int);
+  return (size_t)B * sizeof(int64_t) + (size_t)(4 * B + (B + 1)) * sizeof(int);
 }
 
 // A sequence's tiles and their items.  Full (16-row) tiles all have the same
@@ -656,12 +659,13 @@ __device__ __forceinline__ void seq_locate(const SeqInfo& s, const SeqTiles& st,
   });
 }
 
-// Inclusive sum of (x, y) over the workgroup's threads (sm: NTH int2).
+// Inclusive sum of (x, y) over the workgroup's first `span` threads (sm: NTH
+// int2; rounds only as many as span needs).
 template <int NTH>
-__device__ __forceinline__ int2 block_scan2(int2 v, int2* sm) {
+__device__ __forceinline__ int2 block_scan2(int2 v, int2* sm, int span) {
   sm[threadIdx.x] = v;
   __syncthreads();
-  for (int off = 1; off < NTH; off <<= 1) {
+  for (int off = 1; off < span; off <<= 1) {
     const int2 add = threadIdx.x >= (unsigned)off ? sm[threadIdx.x - off] : int2{0, 0};
     __syncthreads();
     v.x += add.x;
@@ -787,62 +791,76 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
   int* const sm_prior = sm_rows + B;
   int* const sm_order = sm_prior + B;    // position -> sequence
   int* const sm_prefix = sm_order + B;   // B + 1 entries, by position
-  int* const sm_key = sm_prefix + B + 1;  // B <= kRankSeqs: weight per sequence
 
   constexpr int CG = col_group<D>();
-  // Pass 1, sequences b = tid, tid + NTH, ... (B <= kMaxSeqs): tables and
-  // each sequence's item count (parked in sm_prefix[b + 1] until the order
-  // is known) and weight.
-  const bool rank = B <= kRankSeqs;
-  for (int b = threadIdx.x; b < B; b += NTH) {
-    const SeqInfo s = seq_info(p, b);
-    sm_t0[b] = s.t0;
-    sm_slot[b] = (int)s.slot;
-    sm_rows[b] = s.L;
-    sm_prior[b] = s.c;
-    if (blockIdx.x == 0 && ((s.L + 15) >> 4) > p.n_qtiles)
-      set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
-    int n = 0, weight = 0;
-    if (s.L > 0) n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, weight);
-    sm_prefix[b + 1] = n;
-    if (rank) sm_key[b] = n > 0 ? weight : -1;
-  }
-  __syncthreads();
-  // Order: heaviest sequence first (B <= kRankSeqs; ties by b), else by b.
-  if (rank) {
-    int pos = -1, cnt = 0;
-    if ((int)threadIdx.x < B) {
-      const int b = threadIdx.x;
-      const int kb = sm_key[b];
-      cnt = sm_prefix[b + 1];
-      pos = 0;
-      for (int o = 0; o < B; ++o) {
-        const int ko = sm_key[o];
-        pos += (ko > kb || (ko == kb && o < b)) ? 1 : 0;
-      }
-    }
-    __syncthreads();
-    if (pos >= 0) {
-      sm_order[pos] = threadIdx.x;
-      sm_prefix[pos + 1] = cnt;
-    }
-  } else {
-    for (int b = threadIdx.x; b < B; b += NTH) sm_order[b] = b;
-  }
-  __syncthreads();
-  // item prefix over positions
+  MIXED_TRACE(0, 15, __builtin_amdgcn_s_memrealtime());  // workgroup start
   int base = 0;
-  for (int q0 = 0; q0 < B; q0 += NTH) {
-    const int q = q0 + threadIdx.x;
-    const int c = q < B ? sm_prefix[q + 1] : 0;
-    const int2 inc = block_scan2<NTH>(int2{c, 0}, sm_scan);
-    const int tot = sm_scan[NTH - 1].x;
-    if (q < B) sm_prefix[q + 1] = base + inc.x;
-    base += tot;
+  if (B <= kWave) {
+    // A batch of up to 64 sequences: every wave plans it alone, a lane per
+    // sequence, and writes the same tables (identical values from every
+    // wave), reading back only what it wrote itself — no barrier.
+    const int lane = threadIdx.x & (kWave - 1);
+    int n = 0, key = -1;
+    if (lane < B) {
+      const SeqInfo s = seq_info(p, lane);
+      sm_t0[lane] = s.t0;
+      sm_slot[lane] = (int)s.slot;
+      sm_rows[lane] = s.L;
+      sm_prior[lane] = s.c;
+      if (blockIdx.x == 0 && threadIdx.x < kWave && ((s.L + 15) >> 4) > p.n_qtiles)
+        set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
+      int weight = 0;
+      if (s.L > 0) n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, weight);
+      key = n > 0 ? weight : -1;
+    }
+    // position: heaviest sequence first (ties by b)
+    int pos = 0;
+    for (int o = 0; o < B; ++o) {
+      const int ko = __builtin_amdgcn_readlane(key, o);
+      pos += (ko > key || (ko == key && o < lane)) ? 1 : 0;
+    }
+    if (lane < B) sm_order[pos] = lane;
+    const int at = lane < B ? sm_order[lane] : 0;  // the sequence at position `lane`
+    int c = lane < B ? __shfl(n, at, kWave) : 0;
+    // inclusive sum over positions (rounds only as many as B needs)
+    for (int off = 1; off < B; off <<= 1) {
+      const int up = __shfl_up(c, off, kWave);
+      if (lane >= off) c += up;
+    }
+    if (lane < B) sm_prefix[lane + 1] = c;
+    if (lane == 0) sm_prefix[0] = 0;
+    base = __shfl(c, B - 1, kWave);
+  } else {
+    // Larger batches keep their order: per-sequence tables and item counts,
+    // sequences b = tid, tid + NTH, ... (B <= kMaxSeqs), then a block scan.
+    for (int b = threadIdx.x; b < B; b += NTH) {
+      const SeqInfo s = seq_info(p, b);
+      sm_t0[b] = s.t0;
+      sm_slot[b] = (int)s.slot;
+      sm_rows[b] = s.L;
+      sm_prior[b] = s.c;
+      if (blockIdx.x == 0 && ((s.L + 15) >> 4) > p.n_qtiles)
+        set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
+      int n = 0, weight = 0;
+      if (s.L > 0) n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, weight);
+      sm_prefix[b + 1] = n;
+      sm_order[b] = b;
+    }
+    __syncthreads();
+    // item prefix over positions
+    for (int q0 = 0; q0 < B; q0 += NTH) {
+      const int q = q0 + threadIdx.x;
+      const int c = q < B ? sm_prefix[q + 1] : 0;
+      const int span = min(NTH, B - q0);
+      const int2 inc = block_scan2<NTH>(int2{c, 0}, sm_scan, span);
+      const int tot = sm_scan[span - 1].x;
+      if (q < B) sm_prefix[q + 1] = base + inc.x;
+      base += tot;
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) sm_prefix[0] = 0;
     __syncthreads();
   }
-  if (threadIdx.x == 0) sm_prefix[0] = 0;
-  __syncthreads();
   const int n_items = uniform(base);
   const int g = blockIdx.x % p.H_kv;
   const int slot_r = blockIdx.x / p.H_kv;
