@@ -73,7 +73,7 @@ def test_mixed_long_prefixes_split_keys(native_lib, prior, new, d):
 
 
 def test_mixed_largest_batch(native_lib):
-    """1,024 sequences, the kernel's limit: its plan tables (24 B per sequence)
+    """1,024 sequences, the kernel's limit: its plan tables (28 B per sequence)
     take LDS sized to the batch, here the largest allocation it makes."""
     g = torch.Generator().manual_seed(39)
     prior = torch.randint(0, 48, (1024,), generator=g).tolist()
@@ -84,6 +84,26 @@ def test_mixed_largest_batch(native_lib):
     ko, vo = case.appended_pools()
     assert torch.equal(bits(kp), bits(ko)) and torch.equal(bits(vp), bits(vo))
     _check(case, o, "1024 sequences")
+
+
+@pytest.mark.parametrize("B", [64, 65, 200])
+def test_mixed_plan_paths_around_64_sequences(native_lib, B):
+    """Batches of up to 64 sequences are planned by each wave alone (heaviest
+    sequence first), larger ones by the workgroup in sequence order: prefill
+    chunks with long prefixes (split keys), decode rows and empty sequences
+    on both sides of the boundary."""
+    g = torch.Generator().manual_seed(41 + B)
+    prior = torch.randint(0, 2500, (B,), generator=g).tolist()
+    new = [int(x) for x in torch.randint(0, 3, (B,), generator=g)]
+    for i in range(0, B, 9):
+        new[i] = 40 + 7 * (i % 5)  # prefill chunks among the decode rows
+    prior[1] = 9000                   # a prefix long enough to split
+    err = err_word()
+    case = inputs.make_case(prior, new, seed=41 + B)
+    note(f"mixed plan paths B={B} rows={sum(new)}")
+    kp, vp, o = gpu_mixed_step(case, err=err)
+    assert int(err.item()) == 0
+    _check(case, o, f"plan paths B={B}")
 
 
 def test_mixed_batch_above_the_plan_limit_is_rejected(native_lib):
