@@ -778,18 +778,21 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
   __shared__ float2 sm_fml[kFold * kWave];
   __shared__ f16x8 sm_q[CIE_MIXED_QLDS ? col_group<D>() * Geo<D>::KS * kWave : 1];
   __shared__ int sm_last;
-  __shared__ int2 sm_scan[NTH];
-  // The plan, in LDS sized by the launch to the batch (mixed_plan_lds): each
-  // sequence's seq_info, so an item starts its Q and page-id loads without
-  // reading the sequence tables again, the order in which sequences deal
-  // their items, and the item prefix by that order.
+  // block scan (larger batches); a batch of up to 64 sequences ranks
+  // through its first 2 * kWave words
+  __shared__ __attribute__((aligned(16))) int2 sm_scan[NTH];
+  static_assert(NTH >= kWave, "rank keys and item counts fit the scan buffer");
+  // The plan, in LDS sized by the launch to the batch (mixed_plan_lds), all
+  // by position in the order in which sequences deal their items: the
+  // sequence and its seq_info (so an item starts its Q and page-id loads
+  // without reading the sequence tables again), and the item prefix.
   extern __shared__ __attribute__((aligned(16))) char sm_plan[];
   const int B = p.B;
   int64_t* const sm_t0 = reinterpret_cast<int64_t*>(sm_plan);
   int* const sm_slot = reinterpret_cast<int*>(sm_t0 + B);
   int* const sm_rows = sm_slot + B;
   int* const sm_prior = sm_rows + B;
-  int* const sm_order = sm_prior + B;    // position -> sequence
+  int* const sm_order = sm_prior + B;    // the sequence at each position
   int* const sm_prefix = sm_order + B;   // B + 1 entries, by position
 
   constexpr int CG = col_group<D>();
@@ -801,38 +804,50 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     // wave), reading back only what it wrote itself — no barrier.
     const int lane = threadIdx.x & (kWave - 1);
     int n = 0, key = -1;
+    SeqInfo s{0, 0, 0, 0};
     if (lane < B) {
-      const SeqInfo s = seq_info(p, lane);
-      sm_t0[lane] = s.t0;
-      sm_slot[lane] = (int)s.slot;
-      sm_rows[lane] = s.L;
-      sm_prior[lane] = s.c;
+      s = seq_info(p, lane);
       if (blockIdx.x == 0 && threadIdx.x < kWave && ((s.L + 15) >> 4) > p.n_qtiles)
         set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
       int weight = 0;
       if (s.L > 0) n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, weight);
       key = n > 0 ? weight : -1;
     }
-    // position: heaviest sequence first (ties by b)
-    int pos = 0;
-    for (int o = 0; o < B; ++o) {
-      const int ko = __builtin_amdgcn_readlane(key, o);
-      pos += (ko > key || (ko == key && o < lane)) ? 1 : 0;
+    // Position: heaviest sequence first, ties by b.  Rank keys (key + 1,
+    // clamped to 25 bits, above the lane's complement) are distinct, and a
+    // larger one comes earlier; lanes past B write 0, which ranks no one.
+    // Every lane reads all keys and item counts by broadcast LDS reads and
+    // counts the sequences ahead of it and their items: its position and
+    // its item prefix in one pass, with no shuffles.
+    const uint32_t rk =
+        lane < B ? ((uint32_t)min(key + 1, (1 << 25) - 1) << 6) | (uint32_t)(kWave - 1 - lane) : 0u;
+    uint32_t* const sm_rk = reinterpret_cast<uint32_t*>(sm_scan);  // [kWave]
+    int* const sm_rn = reinterpret_cast<int*>(sm_scan) + kWave;     // [kWave]
+    sm_rk[lane] = rk;
+    sm_rn[lane] = n;
+    int pos = 0, before = 0, tot = 0;
+    for (int o = 0; o < B; o += 4) {
+      const uint4 kk = *reinterpret_cast<const uint4*>(sm_rk + o);
+      const int4 nn = *reinterpret_cast<const int4*>(sm_rn + o);
+      pos += (int)(kk.x > rk) + (int)(kk.y > rk) + (int)(kk.z > rk) + (int)(kk.w > rk);
+      before += (kk.x > rk ? nn.x : 0) + (kk.y > rk ? nn.y : 0) + (kk.z > rk ? nn.z : 0) +
+                (kk.w > rk ? nn.w : 0);
+      tot += nn.x + nn.y + nn.z + nn.w;
     }
-    if (lane < B) sm_order[pos] = lane;
-    const int at = lane < B ? sm_order[lane] : 0;  // the sequence at position `lane`
-    int c = lane < B ? __shfl(n, at, kWave) : 0;
-    // inclusive sum over positions (rounds only as many as B needs)
-    for (int off = 1; off < B; off <<= 1) {
-      const int up = __shfl_up(c, off, kWave);
-      if (lane >= off) c += up;
+    if (lane < B) {
+      sm_t0[pos] = s.t0;
+      sm_slot[pos] = (int)s.slot;
+      sm_rows[pos] = s.L;
+      sm_prior[pos] = s.c;
+      sm_order[pos] = lane;
+      sm_prefix[pos + 1] = before + n;
     }
-    if (lane < B) sm_prefix[lane + 1] = c;
     if (lane == 0) sm_prefix[0] = 0;
-    base = __shfl(c, B - 1, kWave);
+    base = tot;
   } else {
-    // Larger batches keep their order: per-sequence tables and item counts,
-    // sequences b = tid, tid + NTH, ... (B <= kMaxSeqs), then a block scan.
+    // Larger batches keep their order (position = sequence): per-sequence
+    // tables and item counts, sequences b = tid, tid + NTH, ...
+    // (B <= kMaxSeqs), then a block scan.
     for (int b = threadIdx.x; b < B; b += NTH) {
       const SeqInfo s = seq_info(p, b);
       sm_t0[b] = s.t0;
@@ -880,10 +895,10 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     const int b = uniform(sm_order[pos]);
     const int j = item - uniform(sm_prefix[pos]);
     SeqInfo s;
-    s.t0 = uniform64(sm_t0[b]);
-    s.slot = uniform(sm_slot[b]);
-    s.L = uniform(sm_rows[b]);
-    s.c = uniform(sm_prior[b]);
+    s.t0 = uniform64(sm_t0[pos]);
+    s.slot = uniform(sm_slot[pos]);
+    s.L = uniform(sm_rows[pos]);
+    s.c = uniform(sm_prior[pos]);
     int qt, jt;
     seq_locate<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, j, qt, jt);
     MIXED_TRACE(item, 1, __builtin_amdgcn_s_memrealtime());
