@@ -49,7 +49,7 @@ MIN_ROTATION_BYTES = 512 << 20
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=800, help="decode calls timed (rounded up to a multiple of R)")
+    ap.add_argument("--steps", type=int, default=800, help="calls timed: exactly K, recorded in one graph (above 4,096, the R-call rotation is replayed and K rounds up to a multiple of R)")
     ap.add_argument("--warmup", type=int, default=80)
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5, 6),
                     help="6: the reference feature bench's mixed shape, beside its published times")
