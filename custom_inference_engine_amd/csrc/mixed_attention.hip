@@ -208,6 +208,17 @@ __device__ __forceinline__ void split_steps(int t_begin, int t_end, int i, int n
   t1 = min(t_end, t_begin + 2 * (int)(steps * (uint32_t)(i + 1) / (uint32_t)n));
 }
 
+// As split_steps, with the remainder steps on the first parts: a tile's last
+// part holds its diagonal (masked) step, so the wave that takes it is not
+// also the one given an extra step.
+__device__ __forceinline__ void split_steps_front(int t_begin, int t_end, int i, int n, int& t0,
+                                                  int& t1) {
+  const uint32_t steps = (uint32_t)(t_end - t_begin + 1) >> 1;
+  const uint32_t un = (uint32_t)n;
+  t0 = min(t_end, t_begin + 2 * (int)((steps * (uint32_t)i + un - 1) / un));
+  t1 = min(t_end, t_begin + 2 * (int)((steps * (uint32_t)(i + 1) + un - 1) / un));
+}
+
 // Q^T operand and key limit of column tile ct (columns = (row, head) pairs).
 template <int D>
 __device__ __forceinline__ void load_combo_q(const MixedParams& p, const SeqInfo& s,
@@ -710,7 +721,7 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   // this chunk's key tiles, and this wave's share of them
   int kt0, kt1, w0, w1;
   split_steps(0, tp.n_ktiles, chunk, tp.n_chunks, kt0, kt1);
-  split_steps(kt0, kt1, wave, W, w0, w1);
+  split_steps_front(kt0, kt1, wave, W, w0, w1);
   const PagedSrc src{p.k_pool,  p.v_pool,  p.block_table + s.slot * p.bt_stride,
                      (int64_t)g * p.pool_head_stride, p.pool_page_stride, p.n_pages,
                      p.page_size, p.err, p.tpp_magic, p.pool_bytes};
