@@ -13,7 +13,8 @@
 // work is laid out as (row, head) columns, G heads per row, packed 16 to an
 // MFMA column tile (attn_engine.h), so K/V bytes are shared by every head and
 // row of the tile inside the MFMA.  One work item is (tile, column group,
-// key chunk): a column group is up to col_group<D>() column tiles, and a
+// key chunk): a column group is up to col_group<D>() column tiles (half as
+// many for a sequence whose tiles all have short key ranges: seq_cg), and a
 // tile's key range [0, kv_len + last row + 1) is cut into chunks only when it
 // is longer than kWavePairs 32-key steps per wave (CIE_MIXED_NARROW_PAIRS for
 // a tile of one column tile, e.g. a decode row).  The item's key tiles are
@@ -45,6 +46,9 @@ namespace cie {
 //                          workgroup), not registers (a wave then fits 256
 //                          registers at D = 64)
 //   CIE_MIXED_WG_PER_CU    workgroups per CU in the grid
+//   CIE_MIXED_SHORT_KTILES a sequence whose longest tile has at most this
+//                          many 16-key tiles uses column groups of half
+//                          CIE_MIXED_CG (0: never)
 #ifndef CIE_MIXED_WAVES
 #define CIE_MIXED_WAVES 4
 #endif
@@ -77,6 +81,9 @@ namespace cie {
 #endif
 #ifndef CIE_MIXED_NARROW_ORDER
 #define CIE_MIXED_NARROW_ORDER 0
+#endif
+#ifndef CIE_MIXED_SHORT_KTILES
+#define CIE_MIXED_SHORT_KTILES 32
 #endif
 
 constexpr int kWavePairs = CIE_MIXED_WAVE_PAIRS;
@@ -171,8 +178,28 @@ __device__ __forceinline__ SeqInfo seq_info(const MixedParams& p, int b) {
 }
 
 struct TilePlan {
-  int row0, rows, n_combos, n_ctiles, n_groups, key_end, n_ktiles, n_pairs, n_chunks;
+  int row0, rows, n_combos, n_ctiles, cg, n_groups, key_end, n_ktiles, n_pairs, n_chunks;
 };
+
+// Column tiles per group for every tile of a sequence: CG, or CG / 2 when
+// the sequence's last (longest) tile has at most CIE_MIXED_SHORT_KTILES key
+// tiles.  Such items are short, so a launch of them is set by latency, and
+// splitting their columns over twice the workgroups shortens it more than
+// the extra K/V reads cost; long tiles keep every K/V byte shared by CG
+// column tiles.  A function of the sequence alone, so the plan, the item
+// lookup and the item agree.
+template <int CG>
+__device__ __forceinline__ int seq_cg(const SeqInfo& s) {
+  if constexpr (CG < 4 || CIE_MIXED_SHORT_KTILES <= 0) return CG;
+  return ((s.c + s.L + 15) >> 4) <= CIE_MIXED_SHORT_KTILES ? CG / 2 : CG;
+}
+
+// Column groups of n column tiles at cg per group (cg = CG or CG / 2: both
+// divisions by constants).
+template <int CG>
+__device__ __forceinline__ int n_col_groups(int n, int cg) {
+  return cg == CG ? (n + CG - 1) / CG : (n + CG / 2 - 1) / (CG / 2);
+}
 
 // CG = column tiles per group, W = wavefronts per workgroup (template
 // arguments, so the chunk count divides by constants: a work item's lookup
@@ -185,7 +212,8 @@ __device__ __forceinline__ TilePlan tile_plan(int qt, const SeqInfo& s, int G) {
   t.rows = min(16, s.L - t.row0);
   t.n_combos = t.rows * G;
   t.n_ctiles = (t.n_combos + 15) >> 4;
-  t.n_groups = (t.n_ctiles + CG - 1) / CG;
+  t.cg = seq_cg<CG>(s);
+  t.n_groups = n_col_groups<CG>(t.n_ctiles, t.cg);
   t.key_end = s.c + t.row0 + t.rows;
   t.n_ktiles = (t.key_end + 15) >> 4;
   t.n_pairs = (t.n_ktiles + 1) >> 1;
@@ -586,7 +614,7 @@ __device__ __forceinline__ SeqTiles seq_tiles(const SeqInfo& s, int n_qtiles, in
   t.n_full = min(s.L >> 4, t.n_tiles);
   t.c16 = (s.c + 15) >> 4;
   t.partial = t.n_tiles > t.n_full;
-  t.ng_full = (G + CG - 1) / CG;
+  t.ng_full = n_col_groups<CG>(G, seq_cg<CG>(s));
   t.full_narrow = G <= 1;
   return t;
 }
@@ -716,8 +744,8 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   const TilePlan tp = tile_plan<CG, W>(qt, s, p.G);
   const int gi = j / tp.n_chunks;
   const int chunk = j - gi * tp.n_chunks;
-  const int ct0 = gi * CG;
-  const int n = min(CG, tp.n_ctiles - ct0);
+  const int ct0 = gi * tp.cg;
+  const int n = min(tp.cg, tp.n_ctiles - ct0);
   // this chunk's key tiles, and this wave's share of them
   int kt0, kt1, w0, w1;
   split_steps(0, tp.n_ktiles, chunk, tp.n_chunks, kt0, kt1);
