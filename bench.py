@@ -40,7 +40,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 # WRITE_SIZE (scale factors from a plain 256 MiB copy), committed under profiles/
 TRAFFIC_BYTES = {
     2: (70_976_000, "profiles/hbm_traffic_decode_config2.md"),
-    3: (39_509_318, "profiles/mixed_attention_config3.md"),
+    3: (39_684_279, "profiles/mixed_attention_config3.md"),
 }
 HBM_PEAK_GBPS = 8000.0
 MIN_ROTATION_BYTES = 512 << 20
