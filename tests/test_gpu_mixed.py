@@ -106,6 +106,25 @@ def test_mixed_plan_paths_around_64_sequences(native_lib, B):
     _check(case, o, f"plan paths B={B}")
 
 
+@pytest.mark.parametrize("h_q,h_kv", [(14, 2), (8, 1), (8, 2)])
+def test_mixed_column_groups_by_sequence(native_lib, h_q, h_kv):
+    """Sequences whose longest tile has at most 32 key tiles (prior + rows <=
+    512) split a tile's columns into groups of 2, longer ones into groups
+    of 4: one batch on both sides of the boundary (full and partial last
+    tiles, a decode row, a prefix long enough to split its keys), for 7, 8
+    and 4 heads per kv head."""
+    prior = [256, 257, 0, 500, 100, 511, 2000, 6000]
+    new = [256, 256, 512, 13, 77, 1, 40, 20]
+    err = err_word()
+    case = inputs.make_case(prior, new, h_q=h_q, h_kv=h_kv, seed=43)
+    note(f"mixed column groups by sequence H_q={h_q} H_kv={h_kv}")
+    kp, vp, o = gpu_mixed_step(case, err=err)
+    assert int(err.item()) == 0
+    ko, vo = case.appended_pools()
+    assert torch.equal(bits(kp), bits(ko)) and torch.equal(bits(vp), bits(vo))
+    _check(case, o, f"column groups H_q={h_q} H_kv={h_kv}")
+
+
 def test_mixed_batch_above_the_plan_limit_is_rejected(native_lib):
     case = inputs.make_case([2] * 1025, seed=40)
     note("mixed 1025 sequences (rejected)")
