@@ -59,6 +59,8 @@ def parse():
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--probe-sweep", action="store_true",
                     help="gather-probe rate by read volume and chunk size (the paged-read ceiling)")
+    ap.add_argument("--probe-cus", action="store_true",
+                    help="gather-probe rate of the decode call's volume on 256 / 128 / 64 CUs (per-CU read limit)")
     ap.add_argument("--repeats", type=int, default=5)
     ap.add_argument("--kernels", action="store_true",
                     help="per-launch times of the append kernels (decode B=32, token T=1052, fused "
@@ -200,6 +202,8 @@ def bench_lib():
         p, i64 = ctypes.c_void_p, ctypes.c_int64
         lib.cie_bench_gather_read.restype = ctypes.c_int
         lib.cie_bench_gather_read.argtypes = [p, p, i64, i64, i64, p, p]
+        lib.cie_bench_gather_read_waves.restype = ctypes.c_int
+        lib.cie_bench_gather_read_waves.argtypes = [p, p, i64, i64, ctypes.c_int, p, p]
         lib.cie_bench_step_probe.restype = ctypes.c_int
         lib.cie_bench_step_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                              ctypes.POINTER(ctypes.c_float)]
@@ -208,10 +212,11 @@ def bench_lib():
 
 
 def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chunk: int = 2048,
-                   region_bytes: int = 1 << 30):
+                   region_bytes: int = 1 << 30, grid: tuple[int, int] | None = None):
     """HBM ceiling of the paged access pattern on this box: the probe kernel reads
     the same byte volume as one decode call as shuffled chunk-sized pieces of a
-    1 GiB region (R disjoint chunk lists rotate, so the 256 MB MALL cannot help)."""
+    1 GiB region (R disjoint chunk lists rotate, so the 256 MB MALL cannot help).
+    grid = (workgroups, waves per workgroup) runs the 2 KiB probe on that grid."""
     from custom_inference_engine_amd import _native
 
     lib = bench_lib()
@@ -225,8 +230,12 @@ def gather_ceiling(dev, nbytes: int, steps: int, warmup: int, repeats: int, chun
 
     def f(i):
         def g():
-            rc = lib.cie_bench_gather_read(region.data_ptr(), lists[i].data_ptr(), n, chunk, 2048,
-                                           sink.data_ptr(), _native.stream_handle(dev))
+            if grid is not None:
+                rc = lib.cie_bench_gather_read_waves(region.data_ptr(), lists[i].data_ptr(), n, grid[0],
+                                                     grid[1], sink.data_ptr(), _native.stream_handle(dev))
+            else:
+                rc = lib.cie_bench_gather_read(region.data_ptr(), lists[i].data_ptr(), n, chunk, 2048,
+                                               sink.data_ptr(), _native.stream_handle(dev))
             if rc != 0:
                 raise RuntimeError(f"cie_bench_gather_read failed: status {rc}")
         return g
@@ -521,6 +530,20 @@ def probe_sweep(args):
               flush=True)
 
 
+def probe_cus(args):
+    """The decode call's K/V volume read as shuffled 2 KiB chunks by the whole chip
+    (256 workgroups of 4 waves, one per CU) and by fewer CUs with more waves each
+    (128 x 8, 64 x 16): whether a (sequence, kv head) can be read by one CU, with no
+    split and no merge (config 2 has 64 of them)."""
+    dev = torch.device("cuda:0")
+    nbytes = 32 * 2 * 4097 * 256  # config 2's K and V bytes
+    for wg, waves in ((256, 4), (128, 8), (64, 16)):
+        us, moved = gather_ceiling(dev, nbytes, 400, 40, 3, 2048, 1 << 30, grid=(wg, waves))
+        print(json.dumps({"probe_bytes": moved, "workgroups": wg, "waves_per_workgroup": waves,
+                          "us": round(us, 2), "TBps": round(moved / us / 1e6, 3),
+                          "GBps_per_cu": round(moved / us / 1e3 / wg, 1)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -534,6 +557,8 @@ def main():
         return copy_calibration(args)
     if args.probe_sweep:
         return probe_sweep(args)
+    if args.probe_cus:
+        return probe_cus(args)
     if args.kernels:
         return bench_kernels(args)
     if args.step_probe:

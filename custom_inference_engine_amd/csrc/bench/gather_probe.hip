@@ -17,8 +17,8 @@ namespace cie_bench {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 
-template <int CHUNK16>  // 16-byte words per chunk (a multiple of 64)
-__global__ __launch_bounds__(256) void gather_read_kernel(const u32x4* __restrict__ base,
+template <int CHUNK16, int MAX_THREADS = 256>  // 16-byte words per chunk (a multiple of 64)
+__global__ __launch_bounds__(MAX_THREADS) void gather_read_kernel(const u32x4* __restrict__ base,
                                                           const int32_t* __restrict__ ids,
                                                           int64_t n_chunks, uint32_t* sink) {
   constexpr int PER_LANE = CHUNK16 / kWave;
@@ -66,5 +66,23 @@ extern "C" int cie_bench_gather_read(const void* base, const int32_t* chunk_ids,
     case 4096: hipLaunchKernelGGL(gather_read_kernel<256>, grid, dim3(256), 0, s, b, chunk_ids, n_chunks, sink); break;
     default: return -2;
   }
+  return (int)hipGetLastError();
+}
+
+// The same read with `waves` wavefronts per workgroup (1..16), 2 KiB chunks:
+// how many CUs the paged read needs (bench.py --probe-cus: the call's volume
+// on 256 workgroups of 4 waves, 128 of 8, 64 of 16).  0 on success, -1 for
+// bad arguments, else the hipError_t of the launch.
+extern "C" int cie_bench_gather_read_waves(const void* base, const int32_t* chunk_ids,
+                                           int64_t n_chunks, int64_t n_workgroups, int waves,
+                                           uint32_t* sink, void* stream) {
+  if (!base || !chunk_ids || !sink || n_chunks < 0 || n_workgroups <= 0 ||
+      n_workgroups > 0x7fffffff || waves < 1 || waves > 16)
+    return -1;
+  if (reinterpret_cast<uintptr_t>(base) & 15) return -1;
+  if (n_chunks == 0) return 0;
+  hipLaunchKernelGGL((gather_read_kernel<128, 1024>), dim3((unsigned)n_workgroups), dim3(64 * waves), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(base), chunk_ids,
+                     n_chunks, sink);
   return (int)hipGetLastError();
 }
