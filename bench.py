@@ -59,6 +59,8 @@ def parse():
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--probe-sweep", action="store_true",
                     help="gather-probe rate by read volume and chunk size (the paged-read ceiling)")
+    ap.add_argument("--variable-lengths", action="store_true",
+                    help="config 2's variant: per-sequence prior lengths uniform in [512, 4096] (seed 0)")
     ap.add_argument("--probe-cus", action="store_true",
                     help="gather-probe rate of the decode call's volume on 256 / 128 / 64 CUs (per-CU read limit)")
     ap.add_argument("--repeats", type=int, default=5)
@@ -315,7 +317,7 @@ def bench_kernels(args):
 
 
 def trace_decode(args):
-    """Phase trace of one config-2 call (append fused) after R warm calls.
+    """Phase trace of one config-2 call (append fused; --variable-lengths: its variant) after R warm calls.
 
     A trace build stamps s_memrealtime (100 MHz) into LDS at phase boundaries
     and each workgroup copies its stamps out as it exits; printed: per phase
@@ -334,7 +336,7 @@ def trace_decode(args):
         raise SystemExit("--trace-decode needs a trace build (see --help)")
     lib.cie_decode_trace_buffer.argtypes = [ctypes.c_void_p]
     dev = torch.device("cuda:0")
-    case = inputs.config2(seed=0)
+    case = inputs.config2(seed=0, fixed=not args.variable_lengths)
     c = case.to(dev)
     S = args.splits or cie.attn.core.default_decode_splits(case.B, 2, dev)
     W, slots = 4, 24
@@ -583,7 +585,8 @@ def main():
         return bench_model(args, cie, dev)
     if args.config == 6:
         return bench_feature_shapes(args, cie, inputs, ref, dev)
-    case = inputs.config2(seed=0) if args.config == 2 else inputs.config4(seed=0)
+    case = (inputs.config2(seed=0, fixed=not args.variable_lengths) if args.config == 2
+            else inputs.config4(seed=0))
     splits = args.splits or (case.meta.get("n_splits") if args.config == 4 else None)
     log(f"config {args.config}: B={case.B} attend={int(case.attended[0])} pool pages={case.k_pool.shape[0]}")
 
@@ -705,8 +708,9 @@ def main():
             "workload": wl,
             "config_id": args.config,
             "batch": case.B,
-            "kv_len_prior": int(case.kv_lens[0]),
-            "attended": attended_list[0],
+            "kv_len_prior": (int(case.kv_lens[0]) if not args.variable_lengths else
+                             f"U[512, 4096] per sequence (sum {int(case.kv_lens.sum())})"),
+            "attended": attended_list[0] if not args.variable_lengths else sum(attended_list),
             "heads_q": 14, "heads_kv": 2, "head_dim": 64, "page_size": 16,
             "pool_pages_per_layer": int(case.k_pool.shape[0]),
             "layer_rotation": R,
