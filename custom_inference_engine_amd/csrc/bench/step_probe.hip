@@ -5,9 +5,10 @@
 // cie_bench_step_probe runs `iters` steps of the math of one wave's 32-key
 // step against 4 column tiles (D = 64) — the pipelined stream's segments:
 // exponentials, P.V MFMAs and S MFMAs of the next step, then the reference-
-// max check — on register-resident operands, one workgroup of 4 waves per
-// CU times `waves_per_simd` (on all CUs or the first n_cus), and returns the
-// time per step (one wave's).
+// max check — on register-resident operands, with `waves_per_simd` waves
+// per SIMD (one workgroup of 4 or 8 waves per CU, so the waves of a CU are
+// co-resident; on all CUs or on n_cus of them), and returns the time per
+// step (one wave's).
 // Modes: 0 the whole step; 1 its 32 MFMAs alone; 2 its softmax VALU work
 // alone (FMA, exponential, conversion, row sums).  Comparing 0 with 1 + 2
 // shows how much of a lone wave's MFMA and VALU work overlaps; comparing
@@ -21,8 +22,8 @@ namespace cie_bench {
 
 using namespace cie;
 
-template <int MODE>
-__global__ __launch_bounds__(256) void step_probe_kernel(float* out, int iters, float scale) {
+template <int MODE, int THREADS>
+__global__ __launch_bounds__(THREADS) void step_probe_kernel(float* out, int iters, float scale) {
   constexpr int D = 64, KS = 2, NT = 4, NCT = 4;
   const int lane = threadIdx.x & 63;
   SoftmaxAcc<D, NCT> st;
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(256) void step_probe_kernel(float* out, int iters, 
     acc += st.l(c) + st.m[c] + s[c][0][0] + s[c][1][3];
     for (int nt = 0; nt < NT; ++nt) acc += st.acc[c][nt][0];
   }
-  out[blockIdx.x * 256 + threadIdx.x] = acc;  // keeps the work
+  out[blockIdx.x * THREADS + threadIdx.x] = acc;  // keeps the work
 }
 
 }  // namespace cie_bench
@@ -124,18 +125,30 @@ extern "C" int cie_bench_step_probe(int mode, int waves_per_simd, int iters, int
   if (hipGetDevice(&dev) == hipSuccess)
     (void)hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
   if (n_cus > 0 && n_cus < n_cu) n_cu = n_cus;
-  const int blocks = n_cu * waves_per_simd;
+  // one workgroup per CU of 4 waves per wanted wave per SIMD, so the waves of
+  // a CU are co-resident (the 512-thread kernel is built to fit two waves per
+  // SIMD); n_cus workgroups land on n_cus different CUs
+  const int blocks = n_cu;
+  const int threads = 256 * waves_per_simd;
   float* out = nullptr;
-  hipError_t e = hipMalloc(&out, (size_t)blocks * 256 * sizeof(float));
+  hipError_t e = hipMalloc(&out, (size_t)blocks * threads * sizeof(float));
   if (e != hipSuccess) return (int)e;
   hipEvent_t a = nullptr, b = nullptr;
   (void)hipEventCreate(&a);
   (void)hipEventCreate(&b);
   auto launch = [&](int n) {
-    switch (mode) {
-      case 0: hipLaunchKernelGGL(step_probe_kernel<0>, dim3(blocks), dim3(256), 0, 0, out, n, 0.18f); break;
-      case 1: hipLaunchKernelGGL(step_probe_kernel<1>, dim3(blocks), dim3(256), 0, 0, out, n, 0.18f); break;
-      default: hipLaunchKernelGGL(step_probe_kernel<2>, dim3(blocks), dim3(256), 0, 0, out, n, 0.18f); break;
+    if (waves_per_simd == 1) {
+      switch (mode) {
+        case 0: hipLaunchKernelGGL((step_probe_kernel<0, 256>), dim3(blocks), dim3(256), 0, 0, out, n, 0.18f); break;
+        case 1: hipLaunchKernelGGL((step_probe_kernel<1, 256>), dim3(blocks), dim3(256), 0, 0, out, n, 0.18f); break;
+        default: hipLaunchKernelGGL((step_probe_kernel<2, 256>), dim3(blocks), dim3(256), 0, 0, out, n, 0.18f); break;
+      }
+    } else {
+      switch (mode) {
+        case 0: hipLaunchKernelGGL((step_probe_kernel<0, 512>), dim3(blocks), dim3(512), 0, 0, out, n, 0.18f); break;
+        case 1: hipLaunchKernelGGL((step_probe_kernel<1, 512>), dim3(blocks), dim3(512), 0, 0, out, n, 0.18f); break;
+        default: hipLaunchKernelGGL((step_probe_kernel<2, 512>), dim3(blocks), dim3(512), 0, 0, out, n, 0.18f); break;
+      }
     }
   };
   launch(10);
