@@ -958,9 +958,42 @@ static int mixed_workgroups(int H_kv) {
   return per_head * H_kv;
 }
 
+// LDS a workgroup may use on the current device (160 KiB on gfx950).
+static int64_t device_lds_limit() {
+  constexpr int kMaxDevices = 64;
+  static int64_t lim[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 160 * 1024;
+  if (lim[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || n <= 0)
+      n = 160 * 1024;
+    lim[dev] = n;
+  }
+  return lim[dev];
+}
+
+template <int D, bool P32>
+static int64_t mixed_static_lds() {
+  static int64_t bytes = -1;
+  if (bytes < 0) {
+    hipFuncAttributes a{};
+    bytes = hipFuncGetAttributes(&a, reinterpret_cast<const void*>(mixed_attention_kernel<D, P32>)) ==
+                    hipSuccess
+                ? (int64_t)a.sharedSizeBytes
+                : 0;
+  }
+  return bytes;
+}
+
 template <int D>
 static int launch_mixed(const MixedParams& p, hipStream_t stream) {
   dim3 grid(mixed_workgroups(p.H_kv), 1, 1);
+  // a batch whose plan tables would take the workgroup past the device's
+  // LDS is refused here (the dispatch itself would be rejected)
+  const int64_t lds = (p.pool_bytes != 0 ? mixed_static_lds<D, true>() : mixed_static_lds<D, false>()) +
+                      (int64_t)mixed_plan_lds(p.B);
+  if (lds > device_lds_limit()) return CIE_EUNSUPPORTED;
   if (p.pool_bytes != 0)
     hipLaunchKernelGGL((mixed_attention_kernel<D, true>), grid, dim3(mixed_waves<D>() * kWave),
                        mixed_plan_lds(p.B), stream, p);
