@@ -238,7 +238,9 @@ int cie_kv_append_tokens_qkv_rope(void* q_out, void* k_pool, void* v_pool,
  *   q, o       : (total_T, H_q, D) dense fp16
  *   max_seqlen : upper bound on every sequence's query length (the
  *                reference's metadata token-count bucket); rows past it are
- *                not computed (CIE_ERRBIT_LEN).  B <= 1024.
+ *                not computed (CIE_ERRBIT_LEN).  B <= 1024 (its plan
+ *                tables live in LDS: a batch that would take a workgroup
+ *                past the device's LDS limit gets CIE_EUNSUPPORTED).
  *   partials   : cie_mixed_partials_bytes(total_T, H_q, D) bytes, 16-byte
  *                aligned, any contents (per-chunk softmax state)
  *   counters   : cie_mixed_counters(B, H_kv, max_seqlen) int32, 16-byte
