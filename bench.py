@@ -649,6 +649,21 @@ def main():
     log(f"call, fused, eager launches: {us_eager:.2f} us")
     us_dec, _ = time_calls([decode_only(i) for i in range(R)], args.steps, args.warmup, use_graph, args.repeats)
     log(f"decode op alone (1 launch): {us_dec:.2f} us")
+    # the Qwen2 drop-in's default decode launch: QKV split + RoPE + append +
+    # split-KV decode from the fused projection's output row (same pools)
+    qkv_rows = [torch.cat([L.q.reshape(1, case.B, -1), L.k_new.reshape(1, case.B, -1),
+                           L.v_new.reshape(1, case.B, -1)], dim=-1).contiguous() for L in layers]
+    gcs = torch.Generator(device=dev).manual_seed(3)
+    cos_t = torch.rand((1, case.B, 64), generator=gcs, device=dev).half()
+    sin_t = torch.rand((1, case.B, 64), generator=gcs, device=dev).half()
+
+    def call_rope(i):
+        L = layers[i]
+        return lambda: cie.decode_qkv_rope_gqa_attention(qkv_rows[i], cos_t, sin_t, L.kp, L.vp, lens_pool,
+                                                         slot_ids, bt, num_heads=14, num_programs=splits)
+    us_rope, _ = time_calls([call_rope(i) for i in range(R)], args.steps, args.warmup, use_graph,
+                            args.repeats)
+    log(f"call, QKV split + RoPE + append + decode (the drop-in's launch): {us_rope:.2f} us")
     us_default = None
     if splits is not None and args.splits is None:
         # the config states its split count; the library's own choice beside it
@@ -698,6 +713,7 @@ def main():
         "us_per_call_eager": round(us_eager, 3),
         "us_per_call_two_launch": round(us_two, 3),
         "us_decode_op_alone": round(us_dec, 3),
+        "us_per_call_qkv_rope": round(us_rope, 3),
         "us_per_call_default_splits": None if us_default is None else round(us_default, 3),
         "higher_is_better": True,
         "scaling": "weak",
