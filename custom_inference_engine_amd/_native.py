@@ -54,7 +54,7 @@ _SIGNATURES = {
          _c_i64p, _c_i64p, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
-    "cie_paged_decode_noalloc_limit": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "cie_paged_decode_noalloc_limit": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "cie_paged_decode_append_noalloc": (
         ctypes.c_int,
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64p,
@@ -82,7 +82,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -72,8 +72,13 @@ __device__ __forceinline__ void rope8(f16x8& lo, f16x8& hi, f16x8 c_lo, f16x8 c_
   for (int j = 0; j < 8; ++j) {
     const float x0 = (float)lo[j];
     const float x1 = (float)hi[j];
-    const float y0 = __builtin_fmaf(x0, (float)c_lo[j], -(x1 * (float)s_lo[j]));
-    const float y1 = __builtin_fmaf(x1, (float)c_hi[j], x0 * (float)s_hi[j]);
+    float y0 = __builtin_fmaf(x0, (float)c_lo[j], -(x1 * (float)s_lo[j]));
+    float y1 = __builtin_fmaf(x1, (float)c_hi[j], x0 * (float)s_hi[j]);
+    // Round to fp32 first: without this barrier the compiler may fuse the
+    // FMA and the fp16 conversion into one v_fma_mixlo_f16, which rounds the
+    // exact sum straight to fp16 and differs from the reference's fp32 ->
+    // fp16 double rounding in the last bit now and then.
+    asm volatile("" : "+v"(y0), "+v"(y1));
     lo[j] = (f16)y0;
     hi[j] = (f16)y1;
   }

@@ -904,13 +904,25 @@ static int device_scratch(hipStream_t stream, char** out) {
 
 }  // namespace cie
 
-extern "C" int64_t cie_paged_decode_noalloc_limit(int64_t H_q, int64_t D, int64_t n_splits) {
-  // largest batch whose partials and counters fit the static scratch (H_kv >= 1)
-  if (H_q <= 0 || D <= 0 || n_splits <= 0) return -1;
-  int64_t lo = 0, hi = kScratchCounterWords / 2;
+// Whether a problem fits the static scratch: the partials (none for one split)
+// and, past one split, 2 * B * H_kv counter words.
+static bool noalloc_fits(int64_t B, int64_t H_q, int64_t H_kv, int64_t D, int64_t n_splits) {
+  if (n_splits == 1) return true;
+  return 2 * B * H_kv <= kScratchCounterWords &&
+         part_layout(B, H_q, D, n_splits).total <= kScratchPartialBytes;
+}
+
+extern "C" int64_t cie_paged_decode_noalloc_limit(int64_t H_q, int64_t H_kv, int64_t D,
+                                                  int64_t n_splits) {
+  // largest batch the entry point accepts: scratch, and the kernel's grid limit
+  if (H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || D <= 0 || n_splits <= 0 ||
+      n_splits > kMaxSplits)
+    return -1;
+  constexpr int64_t kMaxBatch = 65535;
+  int64_t lo = 0, hi = kMaxBatch;
   while (lo < hi) {
     const int64_t mid = (lo + hi + 1) / 2;
-    if (n_splits == 1 || part_layout(mid, H_q, D, n_splits).total <= kScratchPartialBytes)
+    if (noalloc_fits(mid, H_q, H_kv, D, n_splits))
       lo = mid;
     else
       hi = mid - 1;
@@ -927,9 +939,8 @@ extern "C" int cie_paged_decode_append_noalloc(
     int64_t n_slots, int64_t n_splits, int32_t* err, void* stream) {
   if (B < 0 || H_q <= 0 || H_kv <= 0 || D <= 0 || n_splits <= 0) return CIE_EINVAL;
   if (B == 0) return CIE_OK;
-  if (2 * B * H_kv > kScratchCounterWords ||
-      (n_splits > 1 && part_layout(B, H_q, D, n_splits).total > kScratchPartialBytes))
-    return CIE_ESCRATCH;
+  if (n_splits > kMaxSplits || B > 65535) return CIE_EUNSUPPORTED;
+  if (!noalloc_fits(B, H_q, H_kv, D, n_splits)) return CIE_ESCRATCH;
   hipStream_t s = static_cast<hipStream_t>(stream);
   char* ws = nullptr;
   const int rc = device_scratch(s, &ws);

@@ -160,13 +160,17 @@ int cie_paged_decode_append(void* o, const void* q, void* k_pool, void* v_pool,
  * library (4 MiB of split partials plus 16,384 counter words, one copy per
  * GPU, held until the process ends).  The counters are zeroed by a fill
  * kernel on `stream` at the first call on a device and left zero by every
- * completed call.  A problem whose partials (cie_paged_decode_partials_bytes)
- * exceed 4 MiB or with 2 * B * H_kv > 16384 returns CIE_ESCRATCH and launches
- * nothing; cie_paged_decode_noalloc_limit(H_q, D, n_splits) gives the largest
- * B that fits.  Every call on one GPU shares the array: calls that can
- * overlap in time on one GPU (different streams) race and must not be made.
+ * completed call.  A call with n_splits > 1 whose partials
+ * (cie_paged_decode_partials_bytes) exceed 4 MiB or with 2 * B * H_kv > 16384
+ * returns CIE_ESCRATCH and launches nothing (a one-split call uses no
+ * scratch).  cie_paged_decode_noalloc_limit(H_q, H_kv, D, n_splits) gives the
+ * largest B this entry point accepts (the scratch bounds, and the kernel's
+ * B <= 65535), or -1 for arguments no call accepts (n_splits outside
+ * [1, cie_paged_decode_max_splits()], H_q not a multiple of H_kv).  Every
+ * call on one GPU shares the array: calls that can overlap in time on one
+ * GPU (different streams) race and must not be made.
  */
-int64_t cie_paged_decode_noalloc_limit(int64_t H_q, int64_t D, int64_t n_splits);
+int64_t cie_paged_decode_noalloc_limit(int64_t H_q, int64_t H_kv, int64_t D, int64_t n_splits);
 int cie_paged_decode_append_noalloc(void* o, const void* q, void* k_pool, void* v_pool,
                                     const void* k_new, const void* v_new,
                                     int64_t k_tok_stride, int64_t k_head_stride,

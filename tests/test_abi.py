@@ -156,3 +156,40 @@ def test_rope_entry_points_reject_bad_arguments_without_launching(native_lib):
     assert _call_tokens_rope(lib, qkv=24) == -1             # qkv not 16-byte aligned
     assert _call_tokens_rope(lib, T=0) == 0                 # no tokens: no-op
     assert _call_tokens_rope(lib, T=-1) == -1
+
+
+CIE_EUNSUPPORTED, CIE_ESCRATCH = -2, -3
+SCRATCH_PARTIALS, SCRATCH_WORDS = 4 << 20, 16384
+
+
+def _call_noalloc(lib, B, H_q, H_kv, n_splits):
+    # fake, never-dereferenced device addresses: a refused size returns before any device call
+    return lib.cie_paged_decode_append_noalloc(16, 16, 16, 16, 16, 16, 64, 64, 64, 64, 16, 16, 16, B, H_q,
+                                               H_kv, 64, 16, 64, 2048, 1024, 64, 64, 65, n_splits, None, None)
+
+
+@pytest.mark.parametrize("n_splits", [1, 4, 16])
+@pytest.mark.parametrize("h_q,h_kv", [(14, 1), (14, 2), (32, 8)])
+def test_noalloc_limit_is_exact(native_lib, n_splits, h_q, h_kv):
+    """cie_paged_decode_noalloc_limit gives the largest batch the allocation-free entry
+    point accepts: `limit` gets past every size check (here, with no GPU, it then fails at
+    the device), `limit + 1` is refused on the host."""
+    lib = native_lib
+    limit = lib.cie_paged_decode_noalloc_limit(h_q, h_kv, 64, n_splits)
+    assert 0 < limit <= 65535
+    if n_splits == 1:  # no partials, no counters: only the kernel's grid bound
+        assert limit == 65535
+    else:
+        assert lib.cie_paged_decode_partials_bytes(limit, h_q, 64, n_splits) <= SCRATCH_PARTIALS
+        assert 2 * limit * h_kv <= SCRATCH_WORDS
+        assert (lib.cie_paged_decode_partials_bytes(limit + 1, h_q, 64, n_splits) > SCRATCH_PARTIALS
+                or 2 * (limit + 1) * h_kv > SCRATCH_WORDS)
+    assert _call_noalloc(lib, limit + 1, h_q, h_kv, n_splits) in (CIE_ESCRATCH, CIE_EUNSUPPORTED)
+    assert _call_noalloc(lib, limit, h_q, h_kv, n_splits) not in (CIE_ESCRATCH, CIE_EUNSUPPORTED, -1)
+
+
+def test_noalloc_limit_rejects_impossible_arguments(native_lib):
+    lib = native_lib
+    assert lib.cie_paged_decode_noalloc_limit(14, 2, 64, lib.cie_paged_decode_max_splits() + 1) == -1
+    assert lib.cie_paged_decode_noalloc_limit(14, 3, 64, 4) == -1  # H_q not a multiple of H_kv
+    assert lib.cie_paged_decode_noalloc_limit(14, 2, 64, 0) == -1

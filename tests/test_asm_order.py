@@ -110,3 +110,23 @@ def test_partials_complete_before_arrival(src, kernel, tmp_path):
         # except the output o (plain global stores of fp16) and the pool append
         partial_stores = [l for l in body if STORE.match(l) and "dwordx4" in l and "buffer_store" in l]
         assert partial_stores and all("sc1" in l for l in partial_stores), name
+
+
+FMA_MIX_F16 = re.compile(r"^\s*v_(fma|mad)_mix(lo|hi)_f16\b")
+
+
+@pytest.mark.parametrize("src,kernel", [("paged_decode.hip", "decode_kernel"),
+                                         ("kv_append.hip", "rope")])
+def test_rope_rounds_through_fp32(src, kernel, tmp_path):
+    """RoPE outputs are x*cos + rotate_half(x)*sin rounded to fp32 and then to fp16,
+    as the reference's fp32 apply_rotary_pos_emb followed by the fp16 cast.  A fused
+    v_fma_mixlo_f16 / v_fma_mixhi_f16 rounds the exact sum straight to fp16 and
+    differs from that in the last bit now and then, so none may appear in a kernel
+    that rotates (the compiler formed them from the FMA and the conversion until
+    rope8 made the fp32 value opaque)."""
+    asm = _assembly(src, tmp_path)
+    kernels = {n: b for n, b in _kernels(asm).items() if kernel in n}
+    assert kernels, f"no {kernel} kernel in {src}"
+    for name, body in kernels.items():
+        fused = [l.strip() for l in body if FMA_MIX_F16.match(l)]
+        assert not fused, f"{name}: {len(fused)} single-rounding fp16 FMAs, e.g. {fused[0]}"

@@ -74,7 +74,7 @@ def test_noalloc_matches_workspace_entry_point(native_lib, splits):
 
 def test_noalloc_refuses_problems_beyond_its_scratch(native_lib):
     lib = _native.load()
-    limit = lib.cie_paged_decode_noalloc_limit(14, 64, 16)
+    limit = lib.cie_paged_decode_noalloc_limit(14, 2, 64, 16)
     assert 0 < limit < 4096
     assert lib.cie_paged_decode_partials_bytes(limit, 14, 64, 16) <= 4 << 20
     assert lib.cie_paged_decode_partials_bytes(limit + 1, 14, 64, 16) > 4 << 20
