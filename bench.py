@@ -57,8 +57,6 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of graph replay")
     ap.add_argument("--copy-calib", action="store_true")
-    ap.add_argument("--probe-sweep", action="store_true",
-                    help="gather-probe rate by read volume and chunk size (the paged-read ceiling)")
     ap.add_argument("--variable-lengths", action="store_true",
                     help="config 2's variant: per-sequence prior lengths uniform in [512, 4096] (seed 0)")
     ap.add_argument("--probe-cus", action="store_true",
@@ -70,13 +68,14 @@ def parse():
     ap.add_argument("--trace-decode", action="store_true",
                     help="phase trace of one config-2 call; needs a trace build of the library "
                          "(python -m custom_inference_engine_amd._build -D CIE_DECODE_TRACE --out DIR, "
-                         "then CIE_PAGED_LIB=DIR/libcie_paged.so)")
+                         "then --lib DIR/libcie_paged.so)")
     ap.add_argument("--trace-mixed", action="store_true",
                     help="per-item phase trace of one config-3 mixed launch (--config 6: the feature "
-                         "bench's B = 1 shape); needs a trace build (-D CIE_MIXED_TRACE, loaded through "
-                         "CIE_PAGED_LIB)")
-    ap.add_argument("--step-probe", action="store_true",
-                    help="time the mixed kernel's step math alone (MFMA / VALU split, 1 and 2 waves per SIMD)")
+                         "bench's B = 1 shape); needs a trace build (-D CIE_MIXED_TRACE, then --lib)")
+    ap.add_argument("--lib", default=None, metavar="PATH",
+                    help="time this build of libcie_paged.so instead of the in-tree one (a trace or "
+                         "tuning build written by python -m custom_inference_engine_amd._build -D NAME=VALUE "
+                         "--out DIR); the package itself only ever loads the in-tree library")
     ap.add_argument("--trace-out", default=None, metavar="PATH",
                     help="with --trace-mixed: also write every item's stamps to PATH as JSON")
     ap.add_argument("--mixed-part", choices=("all", "prefill", "decode"), default="all",
@@ -206,9 +205,6 @@ def bench_lib():
         lib.cie_bench_gather_read.argtypes = [p, p, i64, i64, i64, p, p]
         lib.cie_bench_gather_read_waves.restype = ctypes.c_int
         lib.cie_bench_gather_read_waves.argtypes = [p, p, i64, i64, ctypes.c_int, p, p]
-        lib.cie_bench_step_probe.restype = ctypes.c_int
-        lib.cie_bench_step_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                             ctypes.POINTER(ctypes.c_float)]
         _bench_lib = lib
     return _bench_lib
 
@@ -490,48 +486,6 @@ def copy_calibration(args):
     print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
 
 
-def step_probe(args):
-    """The mixed kernel's 32-key step math (4 column tiles, D = 64) with no memory
-    traffic: the whole step, its MFMAs alone and its softmax VALU work alone with
-    one wave per SIMD, and the whole step with two waves per SIMD (time per step of
-    one wave; per SIMD, two waves finish two steps in that time)."""
-    import ctypes
-
-    torch.cuda.init()
-    lib = bench_lib()
-    for cus in (0, 8):  # every CU, then 8 CUs (the chip's clock with little power drawn)
-        for mode, wps, what in ((0, 1, "whole step"), (1, 1, "32 MFMAs alone"),
-                                (2, 1, "softmax VALU work alone"), (0, 2, "whole step, 2 waves per SIMD")):
-            us = ctypes.c_float()
-            rc = lib.cie_bench_step_probe(mode, wps, 2000, cus, ctypes.byref(us))
-            if rc != 0:
-                raise RuntimeError(f"cie_bench_step_probe failed: status {rc}")
-            per_simd = us.value / wps
-            print(json.dumps({"probe": "mixed step math", "what": what, "cus": cus or "all",
-                              "waves_per_simd": wps, "us_per_step_per_wave": round(us.value, 4),
-                              "us_per_step_per_simd": round(per_simd, 4),
-                              # a 16x16x32 MFMA keeps the matrix core busy 16 cycles
-                              "implied_GHz_if_mfma_bound": round(32 * 16 / us.value / 1e3, 2)
-                              if mode == 1 else None}), flush=True)
-
-
-def probe_sweep(args):
-    """The gather probe's time per launch by read volume (2 KiB chunks) and by chunk
-    size (64 MB): separates its fixed cost from the DRAM rate of shuffled chunks.
-    Volumes whose R rotating lists fit in the 256 MB MALL are marked cache-resident."""
-    dev = torch.device("cuda:0")
-    region = 2 << 30
-    cases = [(mb << 20, 2048) for mb in (8, 16, 32, 64, 128, 256, 512)]
-    cases += [(64 << 20, 1024), (64 << 20, 4096)]
-    for nbytes, chunk in cases:
-        R = max(1, min(8, (region // chunk) // (nbytes // chunk)))
-        steps = 64 if nbytes >= 256 << 20 else 200
-        us, moved = gather_ceiling(dev, nbytes, steps, 16, 3, chunk, region)
-        print(json.dumps({"probe_bytes": moved, "chunk": chunk, "rotation": R, "us": round(us, 2),
-                          "TBps": round(moved / us / 1e6, 3), "cache_resident": R * moved <= 256 << 20}),
-              flush=True)
-
-
 def probe_cus(args):
     """The decode call's K/V volume read as shuffled 2 KiB chunks by the whole chip
     (256 workgroups of 4 waves, one per CU) and by fewer CUs with more waves each
@@ -555,16 +509,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
+    if args.lib:
+        from custom_inference_engine_amd import _native
+
+        _native.LIB_PATH = os.path.abspath(args.lib)
     if args.copy_calib:
         return copy_calibration(args)
-    if args.probe_sweep:
-        return probe_sweep(args)
     if args.probe_cus:
         return probe_cus(args)
     if args.kernels:
         return bench_kernels(args)
-    if args.step_probe:
-        return step_probe(args)
     if args.trace_decode:
         return trace_decode(args)
     if args.trace_mixed:

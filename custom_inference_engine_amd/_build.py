@@ -8,8 +8,9 @@ bench.py's measurement helpers (``csrc/bench/``) build into a separate
 ``libcie_bench.so`` (``build_bench``); the product library never contains them.
 
 Tuning variants (the kernels' ``CIE_*`` build-time settings) build elsewhere:
-``python -m custom_inference_engine_amd._build -D CIE_MIXED_NARROW_PAIRS=6 --out DIR``
-writes ``DIR/libcie_paged.so``, which the loader takes from ``CIE_PAGED_LIB``.
+``python -m custom_inference_engine_amd._build -D CIE_DECODE_TRACE=1 --out DIR``
+writes ``DIR/libcie_paged.so``, which ``bench.py --lib`` times; the package
+itself loads only the in-tree library.
 """
 from __future__ import annotations
 
@@ -28,7 +29,7 @@ LIB_NAME = "libcie_paged.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 SOURCES = ("capi.hip", "kv_append.hip", "paged_decode.hip", "mixed_attention.hip")
 # bench.py's measurement helpers: a library of their own, never linked into the product
-BENCH_SOURCES = ("bench/gather_probe.hip", "bench/step_probe.hip")
+BENCH_SOURCES = ("bench/gather_probe.hip",)
 BENCH_LIB_PATH = os.path.join(PKG_DIR, "libcie_bench.so")
 ARCH = "gfx950"
 

@@ -16,10 +16,9 @@ import torch
 
 from ._build import LIB_PATH as _BUILT_LIB
 
-# The in-tree build, or a tuning variant of it (a library built from the same
-# sources with other CIE_* settings by `python -m custom_inference_engine_amd._build
-# -D NAME=VALUE --out DIR`), named by CIE_PAGED_LIB.
-LIB_PATH = os.environ.get("CIE_PAGED_LIB") or _BUILT_LIB
+# The in-tree build.  (bench.py --lib times a trace or tuning build by pointing
+# this at it before the first load; nothing in the package reads another path.)
+LIB_PATH = _BUILT_LIB
 
 _c_i64 = ctypes.c_int64
 _c_ptr = ctypes.c_void_p

@@ -63,6 +63,11 @@ _ctr_cache: dict[int, torch.Tensor] = {}
 _ctr_retired: list[torch.Tensor] = []
 
 
+def _device_index(dev) -> int:
+    dev = torch.device(dev)
+    return dev.index if dev.index is not None else torch.cuda.current_device()
+
+
 def split_counters(dev: torch.device, n: int) -> torch.Tensor:
     """The device's persistent split-arrival counters (zeroed once, kept zero by the kernels).
 
@@ -74,14 +79,30 @@ def split_counters(dev: torch.device, n: int) -> torch.Tensor:
     stale word raises ``CIE_ERRBIT_SPLIT`` in ``err``.  Replaced buffers stay
     alive: a captured graph may still point at them.
     """
+    idx = _device_index(dev)
     with _ctr_lock:
-        buf = _ctr_cache.get(dev.index)
+        buf = _ctr_cache.get(idx)
         if buf is None or buf.numel() < n:
             if buf is not None:
                 _ctr_retired.append(buf)
-            buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=dev)
-            _ctr_cache[dev.index] = buf
+            buf = torch.zeros(max(n, 4096), dtype=torch.int32, device=torch.device("cuda", idx))
+            _ctr_cache[idx] = buf
         return buf
+
+
+def reset_split_counters(dev: torch.device) -> None:
+    """Zero the device's persistent split counters (a fill kernel on the current stream).
+
+    Needed only after a call raised ``CIE_ERRBIT_SPLIT``: a stale word inside
+    ``[0, n_splits)`` cannot be told apart from live arrivals, so the kernels
+    cannot be trusted to have cleaned it.  Stream-ordered like the calls."""
+    idx = _device_index(dev)
+    with _ctr_lock:
+        buf = _ctr_cache.get(idx)
+    if buf is not None:
+        # the buffer may have been created under inference mode (captured steps)
+        with torch.inference_mode():
+            buf.zero_()
 
 
 def _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters):

@@ -586,9 +586,12 @@ static_assert(kRankSeqs == kWave, "a batch small enough to rank is planned by on
 // Bytes of the kernel's dynamic LDS: the plan tables of B sequences — t0 as
 // int64; slot, rows, prior, the order and the item prefix (B + 1 entries)
 // as int32.
-static size_t mixed_plan_lds(int B) {
+constexpr size_t mixed_plan_lds(int B) {
   return (size_t)B * sizeof(int64_t) + (size_t)(4 * B + (B + 1)) * sizeof(int);
 }
+
+// LDS one workgroup may allocate on gfx950.
+constexpr size_t kLdsPerWorkgroup = 160 * 1024;
 
 // A sequence's tiles and their items.  Full (16-row) tiles all have the same
 // column groups and a chunk count that grows with the tile index: with
@@ -803,23 +806,47 @@ constexpr int mixed_waves_per_simd() {
   return D <= 64 && (col_group<D>() <= 2 || CIE_MIXED_QLDS) ? 2 : 1;
 }
 
+// The kernel's static LDS, element counts of its arrays: the waves' states
+// in the fold — [slot][d-tile][lane] (acc) and [slot][lane] (m, l), slot =
+// fold_slot(wave, column tile) — the item's Q operands, and the block scan.
+template <int D>
+struct MixedLds {
+  static constexpr int W = mixed_waves<D>();
+  static constexpr int kFold = col_group<D>() * (W - 1);
+  static constexpr int facc = kFold * Geo<D>::NT * kWave;  // f32x4
+  static constexpr int fml = kFold * kWave;                // float2
+  static constexpr int q = CIE_MIXED_QLDS ? col_group<D>() * Geo<D>::KS * kWave : 1;  // f16x8
+  static constexpr int scan = W * kWave;                   // int2
+  static constexpr size_t bytes = facc * sizeof(f32x4) + fml * sizeof(float2) + q * sizeof(f16x8) +
+                                  scan * sizeof(int2) + 16 /* sm_last, aligned */;
+};
+// Every build must be able to plan a batch of kMaxSeqs sequences: its static
+// LDS plus the plan tables of kMaxSeqs sequences fit one workgroup's LDS.  (A
+// build with 8 waves asked for 170,004 bytes at 1,024 sequences, past the
+// 160 KiB a workgroup may have; the launcher's run-time refusal is a second
+// line of defence for devices with less.)
+template <int D>
+constexpr bool mixed_lds_fits() {
+  return MixedLds<D>::bytes + mixed_plan_lds(kMaxSeqs) <= kLdsPerWorkgroup;
+}
+
 template <int D, bool P32>
 __global__ __launch_bounds__(mixed_waves<D>() * kWave)
 __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_attention_kernel(
     MixedParams p) {
   static_assert(col_group<D>() <= 4 && 8 / col_group<D>() <= kMaxColGroups, "column groups");
+  static_assert(mixed_lds_fits<D>(),
+                "static LDS + the plan tables of kMaxSeqs sequences exceed a workgroup's LDS");
   constexpr int W = mixed_waves<D>();
   constexpr int NTH = W * kWave;
-  // the waves' states in the fold: [slot][d-tile][lane] (acc) and
-  // [slot][lane] (m, l), slot = fold_slot(wave, column tile)
-  constexpr int kFold = col_group<D>() * (W - 1);
-  __shared__ f32x4 sm_facc[kFold * Geo<D>::NT * kWave];
-  __shared__ float2 sm_fml[kFold * kWave];
-  __shared__ f16x8 sm_q[CIE_MIXED_QLDS ? col_group<D>() * Geo<D>::KS * kWave : 1];
+  typedef MixedLds<D> Lds;
+  __shared__ f32x4 sm_facc[Lds::facc];
+  __shared__ float2 sm_fml[Lds::fml];
+  __shared__ f16x8 sm_q[Lds::q];
   __shared__ int sm_last;
   // block scan (larger batches); a batch of up to 64 sequences ranks
   // through its first 2 * kWave words
-  __shared__ __attribute__((aligned(16))) int2 sm_scan[NTH];
+  __shared__ __attribute__((aligned(16))) int2 sm_scan[Lds::scan];
   static_assert(NTH >= kWave, "rank keys and item counts fit the scan buffer");
   // The plan, in LDS sized by the launch to the batch (mixed_plan_lds), all
   // by position in the order in which sequences deal their items: the

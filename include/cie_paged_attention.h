@@ -110,7 +110,10 @@ int cie_kv_append_tokens(void* k_pool, void* v_pool,
  *                finds an arrival word outside [0, n_splits) raises
  *                CIE_ERRBIT_SPLIT (its o is then not valid); when every split
  *                of a (sequence, kv head) finds it stale, the call also puts
- *                both words back to zero.
+ *                both words back to zero.  A stale value inside [0, n_splits)
+ *                cannot be told apart from live arrivals and may survive the
+ *                call, so after CIE_ERRBIT_SPLIT the caller zeroes the
+ *                counters before the next call.
  *   partials and counters may be NULL when n_splits == 1.
  */
 int64_t cie_paged_decode_partials_bytes(int64_t B, int64_t H_q, int64_t D,

@@ -215,3 +215,43 @@ def test_decode_ignores_block_table_entries_past_the_sequence(native_lib):
     torch.cuda.synchronize()
     assert int(err.item()) == 0
     assert_attn_close(o[0].float().cpu(), oracle_decode(case), what="garbage past the sequence")
+
+
+def test_decode_counter_preloaded_negative_is_flagged_then_reset(native_lib):
+    """A word just below zero (-1) is flagged on the call that finds it; since the
+    stale value then lands inside [0, n_splits) the caller re-zeroes the counters
+    (reset_split_counters for the library's own buffer), and the next call is
+    correct with no error bit."""
+    from custom_inference_engine_amd.attn.core import reset_split_counters, split_counters
+
+    case = inputs.make_case([300, 1, 2000], seed=32)
+    note("decode counter preloaded -1")
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    want = oracle_decode(case)
+    S = 4
+    for own_buffer in (True, False):
+        if own_buffer:  # a caller-owned buffer, zeroed by the caller
+            ctr = torch.zeros(2 * case.B * 2, dtype=torch.int32, device=DEV)
+        else:  # the library's persistent buffer
+            ctr = split_counters(torch.device(DEV), 2 * case.B * 2)
+        with torch.inference_mode():  # the library's buffer may be an inference tensor
+            ctr[2 * 1 + 0] = -1  # arrival word of (sequence 1, kv head 0)
+        err = err_word()
+        decode_gqa_attention(c.q, kp, vp, c.attended, c.slot_ids, c.block_table, num_programs=S,
+                             counters=ctr if own_buffer else None, err=err)
+        torch.cuda.synchronize()
+        assert int(err.item()) & 8, "CIE_ERRBIT_SPLIT expected"
+        if own_buffer:
+            with torch.inference_mode():
+                ctr.zero_()
+        else:
+            reset_split_counters(torch.device(DEV))
+        assert torch.count_nonzero(ctr) == 0
+        err.zero_()
+        o = decode_gqa_attention(c.q, kp, vp, c.attended, c.slot_ids, c.block_table, num_programs=S,
+                                 counters=ctr if own_buffer else None, err=err)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        assert torch.count_nonzero(ctr) == 0
+        assert_attn_close(o[0].float().cpu(), want, what="call after the reset")

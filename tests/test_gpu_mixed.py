@@ -310,3 +310,29 @@ def test_mixed_stale_counters_are_flagged_and_cleared(native_lib):
     torch.cuda.synchronize()
     assert int(err.item()) == 0
     _check(case, o[0].float().cpu(), "call after the stale one")
+
+
+def test_mixed_counters_preloaded_negative_are_flagged_then_reset(native_lib):
+    """Arrival words at -1 are flagged by the call that finds them; after the caller
+    re-zeroes the buffer the next call is correct with no error bit."""
+    case = inputs.make_case([6000, 0, 2500, 700, 30000], [40, 1, 1, 18, 1], seed=38)
+    note("mixed counters preloaded -1")
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    from custom_inference_engine_amd import mixed_gqa_attention
+    n = _native.load().cie_mixed_counters(case.B, 2, 40)
+    ctr = torch.zeros(n, dtype=torch.int32, device=DEV)
+    ctr[: n // 2] = -1  # every arrival word
+    err = err_word()
+    mixed_gqa_attention(c.q, kp, vp, 40, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
+                        counters=ctr, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 8, "CIE_ERRBIT_SPLIT expected"
+    ctr.zero_()
+    err.zero_()
+    o = mixed_gqa_attention(c.q, kp, vp, 40, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
+                            counters=ctr, err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert torch.count_nonzero(ctr) == 0
+    _check(case, o[0].float().cpu(), "call after the reset")

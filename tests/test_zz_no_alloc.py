@@ -57,6 +57,45 @@ def _run(case, splits, noalloc: bool):
     return kp.cpu(), vp.cpu(), o[0].float().cpu()
 
 
+def test_noalloc_first_call_under_graph_capture(native_lib):
+    """The first call of the process (scratch address lookup and the counters' fill
+    kernel included) recorded into a hipGraph, then replayed twice: each replay
+    appends the new rows once and gives exactly what the workspace entry point
+    gives eagerly.  Placed first: no earlier test in the run calls this entry point."""
+    lib = _native.load()
+    case = inputs.make_case([4095, 17, 900, 2500, 0, 1300, 64, 3000], seed=54)
+    splits = 4
+    note(f"noalloc under capture B={case.B} splits={splits}")
+    k_ref, v_ref, o_ref = _run(case, splits, noalloc=False)
+    c = case.to(DEV)
+    kp, vp = c.k_pool.clone(), c.v_pool.clone()
+    o = torch.full_like(c.q, 3.0)
+    err = err_word()
+    a = _args(case, c, kp, vp, o)
+    g = torch.cuda.CUDAGraph()
+    rcs = []
+    # captures run in inference mode, as the package's StepGraph does (torch's
+    # generator capture state, once created there, cannot be used outside it)
+    with torch.inference_mode(), torch.cuda.graph(g):
+        stream = _native.stream_handle(torch.device(DEV))
+        rcs.append(lib.cie_paged_decode_append_noalloc(*a["head"], *a["tail"], splits, err.data_ptr(),
+                                                        stream))
+    assert rcs == [0], rcs
+    for replay in range(2):
+        kp.copy_(c.k_pool)
+        vp.copy_(c.v_pool)
+        o.fill_(3.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        assert torch.equal(bits(kp.cpu()), bits(k_ref)) and torch.equal(bits(vp.cpu()), bits(v_ref)), replay
+        assert torch.equal(o[0].float().cpu(), o_ref), f"replay {replay} differs from the workspace entry point"
+        # the rows were appended where decode_update puts them, and nowhere else
+        ko, vo = case.appended_pools()
+        assert torch.equal(bits(kp.cpu()), bits(ko)) and torch.equal(bits(vp.cpu()), bits(vo))
+
+
 @pytest.mark.parametrize("splits", [4, 16])
 def test_noalloc_matches_workspace_entry_point(native_lib, splits):
     first = inputs.make_case([4095, 17, 900, 2500, 0, 1300, 64, 3000], seed=51)
