@@ -43,6 +43,7 @@ TRAFFIC_BYTES = {
     3: (39_684_279, "profiles/mixed_attention_config3.md"),
 }
 HBM_PEAK_GBPS = 8000.0
+PLAN_LAYERS = 24  # decode calls per step plan: the layers of config 5's model
 MIN_ROTATION_BYTES = 512 << 20
 
 
@@ -618,6 +619,52 @@ def main():
     us_rope, _ = time_calls([call_rope(i) for i in range(R)], args.steps, args.warmup, use_graph,
                             args.repeats)
     log(f"call, QKV split + RoPE + append + decode (the drop-in's launch): {us_rope:.2f} us")
+    # Planned calls: a decode step makes one plan (decode_plan) for all of its
+    # layers, so the timed sequence launches the plan once per PLAN_LAYERS
+    # calls (Qwen2.5-0.5B has 24 layers), inside the timed region.
+    plan_holder = [None]
+
+    def make_plan():
+        plan_holder[0] = cie.decode_plan(layers[0].kp, lens_pool, slot_ids, bt, append=True,
+                                         num_programs=splits)
+
+    def call_planned(k):
+        L = layers[k % R]
+
+        def f():
+            if k == 0:
+                make_plan()
+            outs[k % R] = cie.decode_append_gqa_attention(L.q, L.kp, L.vp, L.k_new, L.v_new, lens_pool,
+                                                          slot_ids, bt, plan=plan_holder[0])
+        return f
+    make_plan()
+    torch.cuda.synchronize()
+    layers[0].kp.copy_(c.k_pool)
+    layers[0].vp.copy_(c.v_pool)
+    call_planned(0)()  # layer 0, with the plan made as a step's first call makes it
+    torch.cuda.synchronize()
+    err_p = (outs[0][0].float().cpu() - want).abs().max().item()
+    log(f"parity (planned): max abs err {err_p:.2e}")
+    if err_p > 2e-3:
+        raise SystemExit(f"parity check failed (planned: err {err_p})")
+    us_planned, _ = time_calls([call_planned(k) for k in range(PLAN_LAYERS)], args.steps, args.warmup,
+                               use_graph, args.repeats)
+    log(f"call, planned fused append + decode (1 plan per {PLAN_LAYERS} calls): {us_planned:.2f} us")
+
+    def call_rope_planned(k):
+        L = layers[k % R]
+
+        def f():
+            if k == 0:
+                make_plan()
+            cie.decode_qkv_rope_gqa_attention(qkv_rows[k % R], cos_t, sin_t, L.kp, L.vp, lens_pool, slot_ids,
+                                              bt, num_heads=14, plan=plan_holder[0])
+        return f
+    us_rope_planned, _ = time_calls([call_rope_planned(k) for k in range(PLAN_LAYERS)], args.steps,
+                                    args.warmup, use_graph, args.repeats)
+    log(f"call, planned QKV split + RoPE + append + decode (1 plan per {PLAN_LAYERS} calls): "
+        f"{us_rope_planned:.2f} us")
+
     us_default = None
     if splits is not None and args.splits is None:
         # the config states its split count; the library's own choice beside it
@@ -668,6 +715,8 @@ def main():
         "us_per_call_two_launch": round(us_two, 3),
         "us_decode_op_alone": round(us_dec, 3),
         "us_per_call_qkv_rope": round(us_rope, 3),
+        "us_per_call_planned": round(us_planned, 3),
+        "us_per_call_qkv_rope_planned": round(us_rope_planned, 3),
         "us_per_call_default_splits": None if us_default is None else round(us_default, 3),
         "higher_is_better": True,
         "scaling": "weak",

@@ -14,14 +14,17 @@ from .attn.core import (  # noqa: F401
     append_tokens_qkv_rope,
     decode_append_gqa_attention,
     decode_gqa_attention,
+    decode_plan,
     decode_qkv_rope_gqa_attention,
     gqa_decode_append_attention_op,
     gqa_decode_attention_op,
+    gqa_decode_plan_op,
     gqa_decode_qkv_rope_attention_op,
     gqa_mixed_attention_op,
     kv_append_tokens_qkv_rope_op,
     mixed_gqa_attention,
     replace_attention,
+    reset_split_counters,
     use_triton_attention,
 )
 from .attn.metadata import AttentionMetadata  # noqa: F401

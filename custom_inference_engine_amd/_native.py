@@ -71,6 +71,31 @@ _SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_i64p, _c_i64p, _c_i64,
          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
+    "cie_paged_decode_plan_workgroups": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "cie_paged_decode_plan_bytes": (_c_i64, [_c_i64]),
+    "cie_paged_decode_planned_partials_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "cie_paged_decode_plan": (
+        ctypes.c_int,
+        [_c_ptr, _c_i64p, _c_i64p, _c_i64p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
+    "cie_paged_decode_planned": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64p, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
+    "cie_paged_decode_append_planned": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr,
+         _c_i64p, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
+    "cie_paged_decode_qkv_rope_planned": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_i64p, _c_ptr,
+         _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_ptr, _c_ptr],
+    ),
     "cie_mixed_partials_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "cie_mixed_counters": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "cie_mixed_attention": (
@@ -81,7 +106,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -29,6 +29,7 @@ does the split, RoPE and ``KVStorage.mixed_update`` of a mixed step in one.
 from __future__ import annotations
 
 import threading
+from typing import Optional
 
 import torch
 from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention, apply_rotary_pos_emb
@@ -114,6 +115,60 @@ def _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters):
     return partials, counters
 
 
+PLAN_WORDS_PER_WORKGROUP = 8 + 4 * 64  # descriptor + its 4 waves' page ids (int32)
+
+
+def decode_plan(k_cache, lens, slot_ids, block_table, append: bool = True, num_programs=None,
+                err=None) -> torch.Tensor:
+    """One decode step's plan, made once and used by every layer's planned decode.
+
+    The slot ids, lengths and block-table rows of a step are the same for all
+    of its layers, so each sequence's attended length (``lens[slot] + 1`` with
+    ``append``, else ``lens[b]``), its split count (balanced by length over
+    the grid) and every workgroup's page ids are worked out once here; a
+    layer's planned launch then reads its descriptor and page ids in one
+    memory round trip.  ``num_programs`` (splits per sequence) sizes the grid
+    at ``B * H_kv * num_programs`` workgroups; by default about one per CU.
+    Returns an int32 tensor; pass it as ``plan=`` to the decode functions of
+    the same step (same ``append`` mode, block table and lengths)."""
+    N_PAGES, H_kv, PAGE_SIZE, _ = k_cache.shape
+    B = slot_ids.shape[0]
+    _require(N_PAGES == block_table.shape[1], "block_table width must equal n_pages")
+    dev = _native.require_device(k_cache, lens, slot_ids, block_table)
+    lens, slot_ids, block_table = _index(lens), _index(slot_ids), _block_table(block_table)
+    lib = _native.load()
+    P = int(num_programs) if num_programs else 0
+    n_wg = lib.cie_paged_decode_plan_workgroups(max(B, 1), H_kv, P)
+    _require(n_wg > 0, "num_programs outside [1, the kernel's split limit]")
+    plan = torch.empty(n_wg * PLAN_WORDS_PER_WORKGROUP, dtype=torch.int32, device=dev)
+    if B == 0:
+        return plan
+    _native.check(
+        lib.cie_paged_decode_plan(
+            plan.data_ptr(), lens.data_ptr(), slot_ids.data_ptr(), block_table.data_ptr(), B, H_kv,
+            PAGE_SIZE, N_PAGES, block_table.stride(0), block_table.shape[1], lens.shape[0] if append
+            else block_table.shape[0], int(bool(append)), n_wg, _native.ptr(err), _native.stream_handle(dev),
+        ),
+        "cie_paged_decode_plan",
+    )
+    return plan
+
+
+def _plan_workgroups(plan: torch.Tensor) -> int:
+    _require(plan.dtype == torch.int32 and plan.is_contiguous() and plan.dim() == 1
+             and plan.numel() % PLAN_WORDS_PER_WORKGROUP == 0, "plan must come from decode_plan")
+    return plan.numel() // PLAN_WORDS_PER_WORKGROUP
+
+
+def _planned_buffers(lib, dev, B, H_q, H_kv, D, n_wg, counters):
+    partials = torch.empty(lib.cie_paged_decode_planned_partials_bytes(n_wg, H_q, H_kv, D),
+                           dtype=torch.uint8, device=dev)
+    if counters is None:
+        counters = split_counters(dev, 2 * B * H_kv)
+    _require(counters.dtype == torch.int32 and counters.numel() >= 2 * B * H_kv, "counters too small")
+    return partials, counters
+
+
 def _cu_count(dev: torch.device | None) -> int:
     if dev is not None and dev.type == "cuda":
         return torch.cuda.get_device_properties(dev).multi_processor_count
@@ -137,7 +192,7 @@ def _check_pool(q, k, v):
 
 
 def decode_gqa_attention(q, k, v, lens, slot_ids, block_table, num_programs=None,
-                         BLOCK_N=64, num_warps=4, wrap=None, err=None, counters=None):
+                         BLOCK_N=64, num_warps=4, wrap=None, err=None, counters=None, plan=None):
     """Paged GQA decode: ``o[0, b, h] = softmax(q[0, b, h] K^T / sqrt(D)) V`` over ``lens[b]`` tokens.
 
     q: (1, B, H_q, D) fp16 contiguous; k, v: (n_pages, H_kv, page_size, D);
@@ -161,6 +216,19 @@ def decode_gqa_attention(q, k, v, lens, slot_ids, block_table, num_programs=None
     o = torch.empty_like(q)
     if B == 0:
         return o
+    if plan is not None:  # a step's plan (decode_plan with append=False)
+        n_wg = _plan_workgroups(plan)
+        partials, counters = _planned_buffers(lib, dev, B, H_q, H_kv, D, n_wg, counters)
+        _native.check(
+            lib.cie_paged_decode_planned(
+                o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), plan.data_ptr(),
+                block_table.data_ptr(), partials.data_ptr(), counters.data_ptr(), B, H_q, H_kv, D,
+                PAGE_SIZE, N_PAGES, k.stride(0), k.stride(1), block_table.stride(0),
+                block_table.shape[1], n_wg, _native.ptr(err), _native.stream_handle(dev),
+            ),
+            "cie_paged_decode_planned",
+        )
+        return o
     _require(P <= lib.cie_paged_decode_max_splits(), "num_programs above the kernel's split limit")
     partials, counters = _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters)
     _native.check(
@@ -178,7 +246,7 @@ def decode_gqa_attention(q, k, v, lens, slot_ids, block_table, num_programs=None
 
 
 def decode_append_gqa_attention(q, k_cache, v_cache, k, v, lens, slot_ids, block_table,
-                                num_programs=None, err=None, counters=None):
+                                num_programs=None, err=None, counters=None, plan=None):
     """KV append of the new token + paged GQA decode in one launch.
 
     Same result as ``KVStorage.decode_update`` (kv_cache/storage.py:87-122)
@@ -206,6 +274,21 @@ def decode_append_gqa_attention(q, k_cache, v_cache, k, v, lens, slot_ids, block
     lib = _native.load()
     o = torch.empty_like(q)
     if B == 0:
+        return o
+    if plan is not None:  # a step's plan (decode_plan with append=True)
+        n_wg = _plan_workgroups(plan)
+        partials, counters = _planned_buffers(lib, dev, B, H_q, H_kv, D, n_wg, counters)
+        _native.check(
+            lib.cie_paged_decode_append_planned(
+                o.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                kr.data_ptr(), vr.data_ptr(), kr.stride(0), kr.stride(1), vr.stride(0), vr.stride(1),
+                plan.data_ptr(), block_table.data_ptr(), partials.data_ptr(), counters.data_ptr(),
+                B, H_q, H_kv, D, PAGE_SIZE, N_PAGES, k_cache.stride(0), k_cache.stride(1),
+                block_table.stride(0), block_table.shape[1], n_wg,
+                _native.ptr(err), _native.stream_handle(dev),
+            ),
+            "cie_paged_decode_append_planned",
+        )
         return o
     _require(P <= lib.cie_paged_decode_max_splits(), "num_programs above the kernel's split limit")
     partials, counters = _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters)
@@ -246,7 +329,8 @@ def _rope_rows(t: torch.Tensor, n: int, d: int) -> torch.Tensor:
 
 
 def decode_qkv_rope_gqa_attention(qkv, cos, sin, k_cache, v_cache, lens, slot_ids, block_table,
-                                  num_heads: int, num_programs=None, err=None, counters=None):
+                                  num_heads: int, num_programs=None, err=None, counters=None,
+                                  plan=None):
     """Decode step from the fused QKV projection output, one launch.
 
     ``qkv`` (1, B, (H_q + 2·H_kv)·D) is ``F.linear(hidden, qkv_weight, qkv_bias)``
@@ -275,6 +359,21 @@ def decode_qkv_rope_gqa_attention(qkv, cos, sin, k_cache, v_cache, lens, slot_id
     lib = _native.load()
     o = q_like
     if B == 0:
+        return o
+    if plan is not None:  # a step's plan (decode_plan with append=True)
+        n_wg = _plan_workgroups(plan)
+        partials, counters = _planned_buffers(lib, dev, B, H_q, H_kv, D, n_wg, counters)
+        _native.check(
+            lib.cie_paged_decode_qkv_rope_planned(
+                o.data_ptr(), rows.data_ptr(), rows.stride(0), cr.data_ptr(), sr.data_ptr(),
+                cr.stride(0), k_cache.data_ptr(), v_cache.data_ptr(), plan.data_ptr(),
+                block_table.data_ptr(), partials.data_ptr(), counters.data_ptr(),
+                B, H_q, H_kv, D, PAGE_SIZE, N_PAGES, k_cache.stride(0), k_cache.stride(1),
+                block_table.stride(0), block_table.shape[1], n_wg,
+                _native.ptr(err), _native.stream_handle(dev),
+            ),
+            "cie_paged_decode_qkv_rope_planned",
+        )
         return o
     _require(P <= lib.cie_paged_decode_max_splits(), "num_programs above the kernel's split limit")
     partials, counters = _split_buffers(lib, dev, B, H_q, H_kv, D, P, counters)
@@ -402,13 +501,17 @@ def _(q, k, v, lens, slot_ids, block_table):
 def gqa_decode_append_attention_op(
     q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k: torch.Tensor,
     v: torch.Tensor, lens: torch.Tensor, slot_ids: torch.Tensor, block_table: torch.Tensor,
+    plan: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
+    if plan is not None:
+        return decode_append_gqa_attention(q, k_cache, v_cache, k, v, lens, slot_ids, block_table,
+                                           plan=plan)
     return decode_append_gqa_attention(q, k_cache, v_cache, k, v, lens, slot_ids, block_table,
                                        **GQA_DECODE_CONFIG)
 
 
 @gqa_decode_append_attention_op.register_fake
-def _(q, k_cache, v_cache, k, v, lens, slot_ids, block_table):
+def _(q, k_cache, v_cache, k, v, lens, slot_ids, block_table, plan=None):
     return torch.empty_like(q)
 
 
@@ -417,15 +520,31 @@ def _(q, k_cache, v_cache, k, v, lens, slot_ids, block_table):
 def gqa_decode_qkv_rope_attention_op(
     qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor,
     v_cache: torch.Tensor, lens: torch.Tensor, slot_ids: torch.Tensor, block_table: torch.Tensor,
-    num_heads: int,
+    num_heads: int, plan: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
+    if plan is not None:
+        return decode_qkv_rope_gqa_attention(qkv, cos, sin, k_cache, v_cache, lens, slot_ids,
+                                             block_table, num_heads, plan=plan)
     return decode_qkv_rope_gqa_attention(qkv, cos, sin, k_cache, v_cache, lens, slot_ids, block_table,
                                          num_heads, **GQA_DECODE_CONFIG)
 
 
 @gqa_decode_qkv_rope_attention_op.register_fake
-def _(qkv, cos, sin, k_cache, v_cache, lens, slot_ids, block_table, num_heads):
+def _(qkv, cos, sin, k_cache, v_cache, lens, slot_ids, block_table, num_heads, plan=None):
     return qkv.new_empty((1, qkv.shape[1], num_heads, k_cache.shape[-1]))
+
+
+@torch.library.custom_op("inference::gqa_decode_plan", mutates_args=())
+def gqa_decode_plan_op(k_cache: torch.Tensor, lens: torch.Tensor, slot_ids: torch.Tensor,
+                       block_table: torch.Tensor) -> torch.Tensor:
+    """A decode step's plan for its fused-append layers (decode_plan, append=True)."""
+    return decode_plan(k_cache, lens, slot_ids, block_table, append=True)
+
+
+@gqa_decode_plan_op.register_fake
+def _(k_cache, lens, slot_ids, block_table):
+    n_wg = _native.load().cie_paged_decode_plan_workgroups(max(slot_ids.shape[0], 1), k_cache.shape[1], 0)
+    return k_cache.new_empty((n_wg * PLAN_WORDS_PER_WORKGROUP,), dtype=torch.int32)
 
 
 @torch.library.custom_op("inference::kv_append_tokens_qkv_rope", mutates_args=("k_cache", "v_cache"))
@@ -514,7 +633,7 @@ class TritonQwen2Attention(torch.nn.Module):
             if metadata.full_decode:
                 o = gqa_decode_qkv_rope_attention_op(
                     qkv, cos, sin, keys, values, kv_manager.lens, metadata.slot_ids,
-                    kv_manager.block_table, self.num_heads,
+                    kv_manager.block_table, self.num_heads, plan=metadata.decode_plan,
                 )
             else:
                 query_states = kv_append_tokens_qkv_rope_op(
@@ -545,6 +664,7 @@ class TritonQwen2Attention(torch.nn.Module):
             o = gqa_decode_append_attention_op(
                 query_states, kv_manager.keys[self.layer_idx], kv_manager.values[self.layer_idx],
                 key_states, value_states, kv_manager.lens, metadata.slot_ids, kv_manager.block_table,
+                plan=metadata.decode_plan,
             )
         elif metadata.full_decode:
             kv_manager.decode_update(self.layer_idx, metadata.slot_ids, key_states, value_states)

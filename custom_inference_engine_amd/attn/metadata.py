@@ -21,6 +21,9 @@ class AttentionMetadata:
         self.offsets = torch.zeros((token_count,), dtype=torch.long, device=device)
         self.max_seqlen = token_count
         self.full_decode = full_decode
+        # a decode step's plan (inference::gqa_decode_plan), made once per
+        # step by the step module and read by every layer; None: unplanned
+        self.decode_plan = None
 
     def prepare_full_graph(self, batch_size: int) -> None:
         self.slot_ids = torch.zeros((batch_size,), dtype=torch.long, device=self.device)

@@ -66,6 +66,8 @@ struct DecodeParams {
   float* part_l;    // (B, H_q, S)
   float* part_acc;  // (B, H_q, S, D)
   int32_t* counters;  // 2 * (B * H_kv): arrival words, then stale words; zero between calls
+  const int32_t* plan;  // planned launches: the step's plan (cie_paged_decode_plan)
+  int32_t n_wg;         // planned launches: the grid (workgroups) the plan was made for
   int64_t pool_page_stride, pool_head_stride, bt_stride, n_pages;
   int32_t bt_width, n_slots, B, H_q, H_kv, G, page_size, n_splits;
   float scale_log2;
@@ -193,9 +195,27 @@ __device__ __forceinline__ float partial_load(const float* ptr) { return agent_l
 
 constexpr int kMaxSplits = 64;
 
+// Where the split partials of one (sequence, kv head) live: the row of (head
+// h of the group, split s) is base + h * hs + s * ss, and the group's G * S
+// rows are contiguous from base.  Unplanned launches keep (b, head, split)
+// order (hs = S, ss = 1); planned ones index by workgroup, (w_first + s,
+// head) (hs = 1, ss = G), so the partials are sized by the grid.
+struct PartRows {
+  int64_t base;
+  int hs, ss;
+  __device__ __forceinline__ int rel(int h, int s) const { return h * hs + s * ss; }
+};
+
+// A step's plan (cie_paged_decode_plan): per workgroup kPlanDescWords int32
+// — b (-1: idle), g, split, S, slot, L, pos (-1: no append), w_first (the
+// group's first workgroup) — then per workgroup and wave the page ids of the
+// wave's first 64 tiles.
+constexpr int kPlanDescWords = 8;
+constexpr int kPlanWaves = 4;
+
 template <int D, int NTHREADS>
-__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g, int n_states,
-                                             int tid);
+__device__ __forceinline__ void merge_splits(const DecodeParams& p, const PartRows& prow, int b,
+                                             int g, int n_states, int tid);
 
 // Profiling builds only (-DCIE_DECODE_TRACE): phase boundaries
 // (s_memrealtime) are stamped into LDS — LDS writes do not count in vmcnt, so
@@ -209,16 +229,25 @@ __device__ uint64_t* g_decode_trace;
   do {                                                        \
     if ((threadIdx.x & (kWave - 1)) == 0) sm_trace[(k)] = (v); \
   } while (0)
+#if CIE_DECODE_TRACE == 2
+// per-wave stamps only (the single-thread phase stamps off, start excepted)
+#define DECODE_TRACE(k, v)                                 \
+  do {                                                     \
+    if ((k) == 0 || (k) == 5 || (k) == 6)                  \
+      if (threadIdx.x == 0) sm_trace[(k)] = (v);           \
+  } while (0)
+#else
 #define DECODE_TRACE(k, v)                  \
   do {                                      \
     if (threadIdx.x == 0) sm_trace[(k)] = (v); \
   } while (0)
+#endif
 #define DECODE_TRACE_DUMP()                                                                          \
   do {                                                                                               \
     __syncthreads();                                                                                 \
     if (threadIdx.x < kTraceSlots && g_decode_trace != nullptr)                                      \
-      g_decode_trace[((int64_t)(b * p.H_kv + g) * p.n_splits + split) * kTraceSlots + threadIdx.x] = \
-          sm_trace[threadIdx.x];                                                                     \
+      g_decode_trace[(int64_t)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)) *    \
+                         kTraceSlots + threadIdx.x] = sm_trace[threadIdx.x];                         \
   } while (0)
 #else
 #define DECODE_TRACE_LANE0(k, v) \
@@ -234,10 +263,11 @@ __device__ uint64_t* g_decode_trace;
 
 // At D = 64 two waves per SIMD must fit (256 registers a wave), so grids of
 // up to two workgroups per CU stay resident in one round.
-template <int D, int WAVES, bool kAppend, bool kRope>
+template <int D, int WAVES, bool kAppend, bool kRope, bool kPlanned>
 __global__ __launch_bounds__(WAVES * kWave) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1)))
 void decode_kernel(DecodeParams p) {
   static_assert(kAppend || !kRope, "rope mode appends");
+  static_assert(!kPlanned || WAVES == kPlanWaves, "a plan holds the page ids of kPlanWaves waves");
   constexpr int KS = Geo<D>::KS;
   constexpr int NT = Geo<D>::NT;
   __shared__ float sm_m[WAVES][16];
@@ -251,78 +281,91 @@ void decode_kernel(DecodeParams p) {
   __syncthreads();
 #endif
 
-  const int split = blockIdx.x;
-  const int g = blockIdx.y;
-  const int b = blockIdx.z;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int r16 = lane & 15;
   const int grp = lane >> 4;
-  const int S = p.n_splits;
+  const int tpp = p.page_size >> 4;  // 16-key tiles per page
+  const int row_tiles = p.bt_width * tpp;
+  // One page id per lane: a wave of up to 64 tiles (its odd last tile
+  // included) never waits on another block-table load before streaming.
+  constexpr int kSpecTiles = kWave;
 
   DECODE_TRACE(0, __builtin_amdgcn_s_memrealtime());
   DECODE_TRACE(5, (uint64_t)__builtin_amdgcn_s_getreg(0xF804));  // HW_ID
   DECODE_TRACE(6, (uint64_t)__builtin_amdgcn_s_getreg(0xF814));  // XCC_ID
 
-  // Wave gw of the TW waves of this (sequence, kv head) takes key tiles
-  // gw, gw + TW, gw + 2*TW, ...  Its k-th tile's page id is held by lane k
-  // (read back with readlane), so a step never waits on a block-table load,
-  // and the first kSpecTiles ids are fetched as soon as the slot is known —
-  // in parallel with the length, which in append mode is itself a load
-  // indexed by the slot.
-  const int TW = S * WAVES;
-  const int gw = split * WAVES + wave;
-  int64_t slot = p.slot_ids[b];
-  const bool slot_ok = slot >= 0 && slot < p.n_slots;
-  if (!slot_ok) {
-    set_err(p.err, CIE_ERRBIT_PAGE);
-    slot = 0;
-  }
-  const int64_t* bt_row = p.block_table + slot * p.bt_stride;
-  const int tpp = p.page_size >> 4;  // 16-key tiles per page
-  const int row_tiles = p.bt_width * tpp;
-  auto lane_page = [&](int k) -> int {  // page id of this wave's k-th tile
-    const int t = gw + k * TW;
-    if (t >= row_tiles) return 0;
-    int64_t page = bt_row[t / tpp];
-    if (page < 0 || page >= p.n_pages) {
-      set_err(p.err, CIE_ERRBIT_PAGE);
-      page = 0;
-    }
-    return (int)page;
-  };
-  // One page id per lane: a wave of up to 64 tiles (its odd last tile
-  // included) never waits on another block-table load before streaming.
-  constexpr int kSpecTiles = kWave;
-  // Every load of the start goes out before any check: a check's error store
-  // (set_err) may alias later loads as far as the compiler knows, so a check
-  // placed between two loads makes the second wait for the first's data.
-  // Issued together, the first tiles' page ids, the length and Q take one
-  // memory round trip.
-  const int t_spec = gw + lane * TW;
-  const int64_t page_spec = (lane < kSpecTiles && t_spec < row_tiles) ? bt_row[t_spec / tpp] : 0;
-  const int64_t len_raw = kAppend ? p.lens[slot] : p.lens[b];
-  // Q^T operand: column r16 = head g*G + r16 (zero past the group).
+  // The workgroup's work: split `split` of the S of (sequence b, kv head g),
+  // the slot, the L keys to attend (append mode: pos + 1, the new token at
+  // pos), and the page ids of this wave's first kSpecTiles tiles, one per lane.
+  // Wave gw of the TW = S * WAVES waves of the (sequence, kv head) takes key
+  // tiles gw, gw + TW, gw + 2*TW, ...; its k-th tile's page id is held by lane
+  // k (read back with readlane), so a step never waits on a block-table load.
+  int split, g, b, S, L, pos = -1, w_first = 0, pages = 0;
+  int64_t slot;
   f16x8 qop[1][KS];
-  const f16* qrow = p.q + (int64_t)b * p.q_row_stride + (int64_t)(g * p.G + r16) * D + 8 * grp;
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-    qop[0][ks] = (r16 < p.G) ? *reinterpret_cast<const f16x8*>(qrow + 32 * ks) : f16x8{};
   f16x8 cs[KS], sn[KS], knew[KS];
-  if constexpr (kRope) {
-    const f16* crow = p.cos + (int64_t)b * p.cs_stride + 8 * grp;
-    const f16* srow = p.sin + (int64_t)b * p.cs_stride + 8 * grp;
-    const f16* krow = p.k_new + (int64_t)b * p.k_tok_stride + (int64_t)g * p.k_head_stride + 8 * grp;
+  // Q^T operand (column r16 = head g*G + r16, zero past the group), and in
+  // rope mode the new token's cos / sin rows and unrotated K row.
+  auto load_q = [&]() {
+    const f16* qrow = p.q + (int64_t)b * p.q_row_stride + (int64_t)(g * p.G + r16) * D + 8 * grp;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      cs[ks] = *reinterpret_cast<const f16x8*>(crow + 32 * ks);
-      sn[ks] = *reinterpret_cast<const f16x8*>(srow + 32 * ks);
-      knew[ks] = *reinterpret_cast<const f16x8*>(krow + 32 * ks);
+    for (int ks = 0; ks < KS; ++ks)
+      qop[0][ks] = (r16 < p.G) ? *reinterpret_cast<const f16x8*>(qrow + 32 * ks) : f16x8{};
+    if constexpr (kRope) {
+      const f16* crow = p.cos + (int64_t)b * p.cs_stride + 8 * grp;
+      const f16* srow = p.sin + (int64_t)b * p.cs_stride + 8 * grp;
+      const f16* krow = p.k_new + (int64_t)b * p.k_tok_stride + (int64_t)g * p.k_head_stride + 8 * grp;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        cs[ks] = *reinterpret_cast<const f16x8*>(crow + 32 * ks);
+        sn[ks] = *reinterpret_cast<const f16x8*>(srow + 32 * ks);
+        knew[ks] = *reinterpret_cast<const f16x8*>(krow + 32 * ks);
+      }
     }
-  }
-
-  int L, pos = -1;
-  {
+  };
+  if constexpr (kPlanned) {
+    // A step's plan (cie_paged_decode_plan) holds this workgroup's descriptor
+    // and its waves' page ids: one memory round trip, after which Q and the
+    // first K/V tiles go out together.  Its indices were checked when it was
+    // made.
+    const int w = blockIdx.x;
+    const int32_t* d = p.plan + (int64_t)w * kPlanDescWords;
+    pages = p.plan[(int64_t)p.n_wg * kPlanDescWords + ((int64_t)w * kPlanWaves + wave) * kWave + lane];
+    b = d[0];
+    if (b < 0) return;  // a workgroup the plan left idle (uniform)
+    g = d[1];
+    split = d[2];
+    S = d[3];
+    slot = d[4];
+    L = d[5];
+    pos = d[6];
+    w_first = d[7];
+    load_q();
+  } else {
+    split = blockIdx.x;
+    g = blockIdx.y;
+    b = blockIdx.z;
+    S = p.n_splits;
+    // The first kSpecTiles page ids are fetched as soon as the slot is known,
+    // in parallel with the length, which in append mode is itself a load
+    // indexed by the slot.  Every load of the start goes out before any
+    // check: a check's error store (set_err) may alias later loads as far as
+    // the compiler knows, so a check placed between two loads makes the
+    // second wait for the first's data.  Issued together, the first tiles'
+    // page ids, the length and Q take one memory round trip.
+    const int gw0 = split * WAVES + wave;
+    slot = p.slot_ids[b];
+    const bool slot_ok = slot >= 0 && slot < p.n_slots;
+    if (!slot_ok) {
+      set_err(p.err, CIE_ERRBIT_PAGE);
+      slot = 0;
+    }
+    const int64_t* row = p.block_table + slot * p.bt_stride;
+    const int t_spec = gw0 + lane * S * WAVES;
+    const int64_t page_spec = (lane < kSpecTiles && t_spec < row_tiles) ? row[t_spec / tpp] : 0;
+    const int64_t len_raw = kAppend ? p.lens[slot] : p.lens[b];
+    load_q();
     const int64_t cap = (int64_t)row_tiles * 16;
     if constexpr (kAppend) {
       const int64_t prior = len_raw;
@@ -341,20 +384,35 @@ void decode_kernel(DecodeParams p) {
       }
       L = slot_ok ? (int)len : 0;
     }
+    // Speculatively fetched page ids of tiles past the sequence are never
+    // used (and never reported: the row may hold anything there).
+    if (lane < kSpecTiles && t_spec < ((L + 15) >> 4)) {
+      int64_t page = page_spec;
+      if (page < 0 || page >= p.n_pages) {
+        set_err(p.err, CIE_ERRBIT_PAGE);
+        page = 0;
+      }
+      pages = (int)page;
+    }
   }
-  const int n_tiles = (L + 15) >> 4;
-  const int n_mine = n_tiles > gw ? (n_tiles - gw + TW - 1) / TW : 0;
-  // Speculatively fetched page ids of tiles past the sequence are never used
-  // (and never reported: the row may hold anything there).
-  int pages = 0;
-  if (lane < kSpecTiles && t_spec < n_tiles) {
-    int64_t page = page_spec;
+  const int TW = S * WAVES;
+  const int gw = split * WAVES + wave;
+  const int64_t* bt_row = p.block_table + slot * p.bt_stride;
+  auto lane_page = [&](int k) -> int {  // page id of this wave's k-th tile
+    const int t = gw + k * TW;
+    if (t >= row_tiles) return 0;
+    int64_t page = bt_row[t / tpp];
     if (page < 0 || page >= p.n_pages) {
       set_err(p.err, CIE_ERRBIT_PAGE);
       page = 0;
     }
-    pages = (int)page;
-  }
+    return (int)page;
+  };
+  const int n_tiles = (L + 15) >> 4;
+  const int n_mine = n_tiles > gw ? (n_tiles - gw + TW - 1) / TW : 0;
+  // where this workgroup's partial rows live (see PartRows)
+  const PartRows prow = kPlanned ? PartRows{(int64_t)w_first * p.G, 1, p.G}
+                                 : PartRows{((int64_t)b * p.H_q + g * p.G) * S, S, 1};
 
   const PagedSrc src{p.k_pool,  p.v_pool,  bt_row, (int64_t)g * p.pool_head_stride,
                      p.pool_page_stride, p.n_pages, p.page_size, p.err};
@@ -513,9 +571,8 @@ void decode_kernel(DecodeParams p) {
   DECODE_TRACE(8, __builtin_amdgcn_s_memrealtime());
 
   constexpr int D4 = D / 4;
-  const int64_t row0 = ((int64_t)b * p.H_q + g * p.G) * S;  // partial row of (b, head g*G, split 0)
   const __amdgpu_buffer_rsrc_t racc =
-      coherent_rsrc(p.part_acc + row0 * D, (uint32_t)(p.G * S * D * sizeof(float)));
+      coherent_rsrc(p.part_acc + prow.base * D, (uint32_t)(p.G * S * D * sizeof(float)));
   for (int it = threadIdx.x; it < p.G * D4; it += WAVES * kWave) {
     const int h = it / D4;
     const int d4 = it - h * D4;
@@ -539,11 +596,11 @@ void decode_kernel(DecodeParams p) {
       for (int i = 0; i < 4; ++i) o4[i] = (f16)(none ? 0.f : num[i] / den);
       *reinterpret_cast<f16x4*>(p.o + ((int64_t)b * p.H_q + g * p.G + h) * D + 4 * d4) = o4;
     } else {
-      const int row = h * S + split;  // within (b, g)
+      const int row = prow.rel(h, split);  // within the group's rows
       agent_store4(racc, (uint32_t)((row * D + 4 * d4) * sizeof(float)), num);
       if (d4 == 0) {
-        partial_store(&p.part_m[row0 + row], M);
-        partial_store(&p.part_l[row0 + row], den);
+        partial_store(&p.part_m[prow.base + row], M);
+        partial_store(&p.part_l[prow.base + row], den);
       }
     }
   }
@@ -561,7 +618,7 @@ void decode_kernel(DecodeParams p) {
     DECODE_TRACE_DUMP();
     return;
   }
-  merge_splits<D, WAVES * kWave>(p, b, g, S, threadIdx.x);
+  merge_splits<D, WAVES * kWave>(p, prow, b, g, S, threadIdx.x);
   if (threadIdx.x == 0) counter_reset(arrival);
   DECODE_TRACE(4, __builtin_amdgcn_s_memrealtime());
   DECODE_TRACE_DUMP();
@@ -576,17 +633,15 @@ void decode_kernel(DecodeParams p) {
 constexpr int kMergeGroup = 8;
 
 template <int D, int NTHREADS>
-__device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g, int n_states,
-                                             int tid) {
+__device__ __forceinline__ void merge_splits(const DecodeParams& p, const PartRows& prow, int b,
+                                             int g, int n_states, int tid) {
   constexpr int D4 = D / 4;
   const int S = n_states;
-  const int64_t row0 = ((int64_t)b * p.H_q + g * p.G) * S;
   const __amdgpu_buffer_rsrc_t racc =
-      coherent_rsrc(p.part_acc + row0 * D, (uint32_t)(p.G * S * D * sizeof(float)));
+      coherent_rsrc(p.part_acc + prow.base * D, (uint32_t)(p.G * S * D * sizeof(float)));
   for (int it = tid; it < p.G * D4; it += NTHREADS) {
     const int h = it / D4;
     const int d4 = it - h * D4;
-    const int r0 = h * S;  // partial row of (h, split 0) within (b, g)
     float M = kNegInf, den = 0.f;
     f32x4 num = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < S; s0 += kMergeGroup) {
@@ -598,9 +653,10 @@ __device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g
         ls[u] = 0.f;
         as[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (s0 + u < S) {
-          ms[u] = partial_load(&p.part_m[row0 + r0 + s0 + u]);
-          ls[u] = partial_load(&p.part_l[row0 + r0 + s0 + u]);
-          as[u] = agent_load4(racc, (uint32_t)(((r0 + s0 + u) * D + 4 * d4) * sizeof(float)));
+          const int row = prow.rel(h, s0 + u);
+          ms[u] = partial_load(&p.part_m[prow.base + row]);
+          ls[u] = partial_load(&p.part_l[prow.base + row]);
+          as[u] = agent_load4(racc, (uint32_t)((row * D + 4 * d4) * sizeof(float)));
         }
       }
       float Mn = M;
@@ -625,6 +681,275 @@ __device__ __forceinline__ void merge_splits(const DecodeParams& p, int b, int g
     for (int i = 0; i < 4; ++i) o4[i] = (f16)(none ? 0.f : num[i] / den);
     *reinterpret_cast<f16x4*>(p.o + ((int64_t)b * p.H_q + g * p.G + h) * D + 4 * d4) = o4;
   }
+}
+
+// ---------------------------------------------------------------------------
+// A decode step's plan.  The slot ids, lengths and block-table rows a decode
+// reads are the same for every layer of a step (the lengths advance after
+// the last layer), so one small launch per step works out what each layer's
+// launch would otherwise redo: every sequence's attended length, how many
+// workgroups (splits) each (sequence, kv head) gets, and each workgroup's
+// page ids.  A planned decode launch then needs one memory round trip (its
+// descriptor and its waves' page ids) before its first K/V loads, where an
+// unplanned one needs two (slot id, then page ids and length).
+//
+// Splits are balanced by length: tau, the smallest tile count per split for
+// which sum_b max(1, ceil(tiles_b / tau)) splits (at most kMaxSplits each)
+// fit the grid's n_wg / H_kv workgroups per kv head, gives sequence b
+// ceil(tiles_b / tau) splits, so the longest sequences no longer set the call
+// when lengths differ.  Equal lengths get equal splits (the unplanned deal).
+// Every workgroup of the plan launch redoes the balance (a few hundred
+// sequences at most, LDS only) and then writes its own descriptor and page
+// ids: no workgroup waits on another.
+constexpr int kPlanMaxSeqs = 1024;
+constexpr int kPlanThreads = kPlanWaves * kWave;
+
+struct PlanParams {
+  int32_t* plan;
+  const int64_t* lens;  // append: (n_slots,) prior length per slot; plain: (B,) attended
+  const int64_t* slot_ids;
+  const int64_t* block_table;
+  int64_t bt_stride, n_pages;
+  int32_t B, H_kv, page_size, bt_width, n_slots, n_wg, append;
+  int32_t* err;
+};
+
+__device__ __forceinline__ int plan_block_sum(int x, int* sm_red) {
+  for (int off = 1; off < kWave; off <<= 1) x += __shfl_xor(x, off, kWave);
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) sm_red[threadIdx.x / kWave] = x;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int w = 0; w < kPlanWaves; ++w) t += sm_red[w];
+  return t;
+}
+
+// A sequence's attended length as the decode kernel derives it (with its
+// index checks; `report` lets one workgroup of the plan report errors).
+__device__ __forceinline__ int plan_seq(const PlanParams& p, int bb, int64_t cap, bool report,
+                                        int* slot_out) {
+  int64_t slot = p.slot_ids[bb];
+  const bool slot_ok = slot >= 0 && slot < p.n_slots;
+  if (!slot_ok) {
+    if (report) set_err(p.err, CIE_ERRBIT_PAGE);
+    slot = 0;
+  }
+  const int64_t len = p.append ? p.lens[slot] : p.lens[bb];
+  int L;
+  if (p.append) {
+    if (!slot_ok || len < 0 || len + 1 > cap) {
+      if (slot_ok && report) set_err(p.err, CIE_ERRBIT_LEN);
+      L = 0;
+    } else {
+      L = (int)len + 1;
+    }
+  } else {
+    int64_t l = len;
+    if (l < 0 || l > cap) {
+      if (report) set_err(p.err, CIE_ERRBIT_LEN);
+      l = l < 0 ? 0 : cap;
+    }
+    L = slot_ok ? (int)l : 0;
+  }
+  *slot_out = (int)slot;
+  return L;
+}
+
+__device__ __forceinline__ int plan_splits(int nt, int tau) {
+  return min(kMaxSplits, max(1, (nt + tau - 1) / tau));
+}
+
+// Writes workgroup w's descriptor (desc[0..7], lanes 0..7 of one wave) and the
+// page ids of wave j (one per lane k) of that workgroup.
+__device__ __forceinline__ void plan_write(const PlanParams& p, int w, int j, int lane, int bb,
+                                           int nt, int S, int w0, int slot, int L, int tpp) {
+  const int g = (w - w0) / S;
+  const int split = (w - w0) - g * S;
+  if (j == 0 && lane < kPlanDescWords) {
+    const int v[kPlanDescWords] = {bb, g, split, S, slot, L, p.append && L > 0 ? L - 1 : -1,
+                                   w0 + g * S};
+    int x = v[0];
+#pragma unroll
+    for (int i = 1; i < kPlanDescWords; ++i) x = lane == i ? v[i] : x;
+    p.plan[(int64_t)w * kPlanDescWords + lane] = x;
+  }
+  // wave j of split s deals tiles (s * kPlanWaves + j) + k * S * kPlanWaves
+  const int t = split * kPlanWaves + j + lane * S * kPlanWaves;
+  int page = 0;
+  if (t < nt) {
+    int64_t pg = p.block_table[(int64_t)slot * p.bt_stride + t / tpp];
+    if (pg < 0 || pg >= p.n_pages) {
+      set_err(p.err, CIE_ERRBIT_PAGE);
+      pg = 0;
+    }
+    page = (int)pg;
+  }
+  p.plan[(int64_t)p.n_wg * kPlanDescWords + ((int64_t)w * kPlanWaves + j) * kWave + lane] = page;
+}
+
+// Batches of up to kWave sequences: every wave plans alone, a sequence per
+// lane (shuffle reductions and scan, no LDS, no barrier).  The search for tau
+// starts at its lower bound ceil(sum of tiles / workgroups per kv head): a
+// split count sum over sequences is at least tiles / tau, so no smaller tau
+// fits; with equal lengths the bound itself fits.
+__device__ __forceinline__ void plan_wave(const PlanParams& p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int j = threadIdx.x / kWave;
+  const int B = p.B;
+  const int tpp = p.page_size >> 4;
+  const int64_t cap = (int64_t)p.bt_width * tpp * 16;
+  int slot = 0, L = 0;
+  if (lane < B) L = plan_seq(p, lane, cap, blockIdx.x == 0 && j == 0, &slot);
+  const int nt = (L + 15) >> 4;
+  int total = lane < B ? nt : 0, hi = nt;
+  for (int off = 1; off < kWave; off <<= 1) {
+    total += __shfl_xor(total, off, kWave);
+    hi = max(hi, __shfl_xor(hi, off, kWave));
+  }
+  const int n_ph = p.n_wg / p.H_kv;
+  auto fits = [&](int tau) {
+    int c = lane < B ? plan_splits(nt, tau) : 0;
+    for (int off = 1; off < kWave; off <<= 1) c += __shfl_xor(c, off, kWave);
+    return c <= n_ph;
+  };
+  int lo = max(1, (total + n_ph - 1) / n_ph);
+  hi = max(hi, lo);
+  if (!fits(lo)) {  // binary search in (lo, hi]; hi always fits (one split each)
+    while (lo + 1 < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (fits(mid))
+        hi = mid;
+      else
+        lo = mid;
+    }
+    lo = hi;
+  }
+  const int tau = lo;
+  // first workgroup of each sequence: exclusive scan of H_kv * splits
+  const int S_b = lane < B ? plan_splits(nt, tau) : 0;
+  int x = p.H_kv * S_b;
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  const int w0_b = x - p.H_kv * S_b;
+  const int used = __shfl(x, kWave - 1, kWave);
+  const int w = blockIdx.x;
+  if (w >= used) {
+    if (j == 0 && lane == 0) p.plan[(int64_t)w * kPlanDescWords] = -1;
+    return;
+  }
+  // my sequence: the last lane whose first workgroup is at or before w
+  const uint64_t at_or_before = __ballot(lane < B && w0_b <= w);
+  const int bb = __popcll(at_or_before) - 1;
+  plan_write(p, w, j, lane, bb, __shfl(nt, bb, kWave), __shfl(S_b, bb, kWave), __shfl(w0_b, bb, kWave),
+             __shfl(slot, bb, kWave), __shfl(L, bb, kWave), tpp);
+}
+
+__global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(PlanParams p) {
+  if (p.B <= kWave) {
+    plan_wave(p);
+    return;
+  }
+  __shared__ int sm_nt[kPlanMaxSeqs];       // key tiles of sequence b (L + 15) / 16
+  __shared__ int sm_len[kPlanMaxSeqs];      // attended keys L
+  __shared__ int sm_slot[kPlanMaxSeqs];
+  __shared__ int sm_w0[kPlanMaxSeqs + 1];   // first workgroup of sequence b
+  __shared__ int sm_red[kPlanWaves];
+  const int tid = threadIdx.x;
+  const int B = p.B;
+  const int tpp = p.page_size >> 4;
+  const int row_tiles = p.bt_width * tpp;
+  const int64_t cap = (int64_t)row_tiles * 16;
+  // index errors are reported once, by workgroup 0 (every workgroup sees them)
+  const bool report = blockIdx.x == 0;
+
+  // 1. every sequence's slot and attended length, with the decode kernel's checks
+  int my_max = 0;
+  for (int bb = tid; bb < B; bb += kPlanThreads) {
+    int slot;
+    const int L = plan_seq(p, bb, cap, report, &slot);
+    const int nt = (L + 15) >> 4;
+    sm_nt[bb] = nt;
+    sm_len[bb] = L;
+    sm_slot[bb] = slot;
+    my_max = max(my_max, nt);
+  }
+  for (int off = 1; off < kWave; off <<= 1) my_max = max(my_max, __shfl_xor(my_max, off, kWave));
+  __syncthreads();
+  if ((tid & (kWave - 1)) == 0) sm_red[tid / kWave] = my_max;
+  __syncthreads();
+  int hi = 1;
+#pragma unroll
+  for (int w = 0; w < kPlanWaves; ++w) hi = max(hi, sm_red[w]);
+
+  // 2. the smallest tiles-per-split tau whose splits fit n_wg / H_kv per kv head
+  const int n_ph = p.n_wg / p.H_kv;
+  auto splits_of = [](int nt, int tau) { return plan_splits(nt, tau); };
+  int lo = 1;
+  while (lo < hi) {  // uniform: every thread holds the same bounds
+    const int mid = (lo + hi) >> 1;
+    int c = 0;
+    for (int bb = tid; bb < B; bb += kPlanThreads) c += splits_of(sm_nt[bb], mid);
+    if (plan_block_sum(c, sm_red) <= n_ph)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  const int tau = lo;
+
+  // 3. first workgroup of each sequence: exclusive prefix of H_kv * splits,
+  // four consecutive sequences per thread
+  {
+    int v[4], run = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int bb = 4 * tid + u;
+      v[u] = bb < B ? p.H_kv * splits_of(sm_nt[bb], tau) : 0;
+      run += v[u];
+    }
+    // inclusive scan of run over the block
+    int x = run;
+    const int lane = tid & (kWave - 1);
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int y = __shfl_up(x, off, kWave);
+      if (lane >= off) x += y;
+    }
+    __syncthreads();
+    if (lane == kWave - 1) sm_red[tid / kWave] = x;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < tid / kWave; ++w) base += sm_red[w];
+    int e = base + x - run;  // exclusive prefix of this thread's first sequence
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int bb = 4 * tid + u;
+      if (bb < B) sm_w0[bb] = e;
+      e += v[u];
+    }
+    if (tid == kPlanThreads - 1) sm_w0[B] = base + x;  // total (sequences past B add 0)
+  }
+  __syncthreads();
+
+  // 4. this workgroup's entry
+  const int w = blockIdx.x;
+  int32_t* const desc = p.plan + (int64_t)w * kPlanDescWords;
+  if (w >= sm_w0[B]) {  // idle: the grid has more workgroups than the balance uses
+    if (tid == 0) desc[0] = -1;
+    return;
+  }
+  int lo_b = 0, hi_b = B - 1;  // the sequence with sm_w0[b] <= w < sm_w0[b + 1]
+  while (lo_b < hi_b) {
+    const int mid = (lo_b + hi_b + 1) >> 1;
+    if (sm_w0[mid] <= w)
+      lo_b = mid;
+    else
+      hi_b = mid - 1;
+  }
+  const int bb = lo_b;
+  plan_write(p, w, tid / kWave, tid & (kWave - 1), bb, sm_nt[bb], splits_of(sm_nt[bb], tau), sm_w0[bb],
+             sm_slot[bb], sm_len[bb], tpp);
 }
 
 // Waves per workgroup: four, one per SIMD.  With the non-temporal K/V loads
@@ -657,17 +982,23 @@ static int device_cus() {
 template <int D, int W, bool kAppend, bool kRope>
 static int launch_decode_waves(const DecodeParams& p, hipStream_t stream) {
   dim3 grid(p.n_splits, p.H_kv, p.B);
-  hipLaunchKernelGGL((decode_kernel<D, W, kAppend, kRope>), grid, dim3(W * kWave), 0, stream, p);
+  hipLaunchKernelGGL((decode_kernel<D, W, kAppend, kRope, false>), grid, dim3(W * kWave), 0, stream, p);
   return (int)hipGetLastError();
 }
 
-template <int D, bool kAppend, bool kRope>
+template <int D, bool kAppend, bool kRope, bool kPlanned>
 static int launch_decode(const DecodeParams& p, hipStream_t stream) {
-  constexpr int W = decode_waves<D>();
-  constexpr int Wh = W > 4 ? W / 2 : W;
-  const int64_t n_wg = (int64_t)p.n_splits * p.H_kv * p.B;
-  return (Wh != W && n_wg > device_cus()) ? launch_decode_waves<D, Wh, kAppend, kRope>(p, stream)
-                                          : launch_decode_waves<D, W, kAppend, kRope>(p, stream);
+  if constexpr (kPlanned) {  // one workgroup per plan entry, kPlanWaves waves each
+    hipLaunchKernelGGL((decode_kernel<D, kPlanWaves, kAppend, kRope, true>), dim3(p.n_wg),
+                       dim3(kPlanWaves * kWave), 0, stream, p);
+    return (int)hipGetLastError();
+  } else {
+    constexpr int W = decode_waves<D>();
+    constexpr int Wh = W > 4 ? W / 2 : W;
+    const int64_t n_wg = (int64_t)p.n_splits * p.H_kv * p.B;
+    return (Wh != W && n_wg > device_cus()) ? launch_decode_waves<D, Wh, kAppend, kRope>(p, stream)
+                                            : launch_decode_waves<D, W, kAppend, kRope>(p, stream);
+  }
 }
 
 // Partials buffer: part_m | part_l | part_acc (fp32), each region 256-byte aligned.
@@ -675,9 +1006,9 @@ struct PartLayout {
   int64_t m, l, acc, total;
 };
 
-static PartLayout part_layout(int64_t B, int64_t H_q, int64_t D, int64_t S) {
+// rows: B * H_q * S for an unplanned launch, n_workgroups * G for a planned one
+static PartLayout part_layout_rows(int64_t rows, int64_t D) {
   auto up = [](int64_t x) { return (x + 255) & ~int64_t(255); };
-  const int64_t rows = B * H_q * S;
   PartLayout w;
   w.m = 0;
   w.l = up(rows * 4);
@@ -685,22 +1016,35 @@ static PartLayout part_layout(int64_t B, int64_t H_q, int64_t D, int64_t S) {
   w.total = up(w.acc + rows * D * 4);
   return w;
 }
+static PartLayout part_layout(int64_t B, int64_t H_q, int64_t D, int64_t S) {
+  return part_layout_rows(B * H_q * S, D);
+}
 
-template <bool kAppend, bool kRope>
+// n_splits: the split count of an unplanned launch, or the workgroups of a
+// planned one (p.plan set; lens / slot_ids / n_slots then unused).
+template <bool kAppend, bool kRope, bool kPlanned = false>
 static int decode_entry(DecodeParams& p, void* partials, int32_t* counters, int64_t B,
                         int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size, int64_t n_pages,
                         int64_t pool_page_stride, int64_t pool_head_stride, int64_t bt_stride,
                         int64_t bt_width, int64_t n_slots, int64_t n_splits, int32_t* err,
                         void* stream) {
   if (B < 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || n_pages <= 0 || bt_width <= 0 ||
-      bt_stride < bt_width || n_slots <= 0 || n_splits <= 0 || page_size <= 0)
+      bt_stride < bt_width || (!kPlanned && n_slots <= 0) || n_splits <= 0 || page_size <= 0)
     return CIE_EINVAL;
   if (B == 0) return CIE_OK;
-  if (!p.o || !p.q || !p.k_pool || !p.v_pool || !p.lens || !p.slot_ids || !p.block_table)
-    return CIE_EINVAL;
-  if (n_splits > 1 && (!partials || !counters)) return CIE_EINVAL;
+  if (!p.o || !p.q || !p.k_pool || !p.v_pool || !p.block_table) return CIE_EINVAL;
+  if (kPlanned ? !p.plan : (!p.lens || !p.slot_ids)) return CIE_EINVAL;
   const int64_t G = H_q / H_kv;
-  if (G > 16 || page_size % 16 != 0 || B > 65535 || H_kv > 65535 || n_splits > kMaxSplits ||
+  if constexpr (kPlanned) {
+    // every (sequence, kv head) has at least one workgroup, at most kMaxSplits
+    if (n_splits < B * H_kv || n_splits % H_kv != 0 || n_splits > B * H_kv * kMaxSplits)
+      return CIE_EINVAL;
+    if (n_splits > B * H_kv && (!partials || !counters)) return CIE_EINVAL;
+  } else {
+    if (n_splits > 1 && (!partials || !counters)) return CIE_EINVAL;
+  }
+  if (G > 16 || page_size % 16 != 0 || B > 65535 || H_kv > 65535 ||
+      (!kPlanned && n_splits > kMaxSplits) || n_splits > 0x7fffffff ||
       bt_width * page_size > 0x7fffffff)
     return CIE_EUNSUPPORTED;
   if (D != 64 && D != 128) return CIE_EUNSUPPORTED;
@@ -711,7 +1055,7 @@ static int decode_entry(DecodeParams& p, void* partials, int32_t* counters, int6
     return CIE_EINVAL;
   if (pool_page_stride % 8 != 0 || pool_head_stride % 8 != 0) return CIE_EINVAL;
 
-  const PartLayout w = part_layout(B, H_q, D, n_splits);
+  const PartLayout w = kPlanned ? part_layout_rows(n_splits * G, D) : part_layout(B, H_q, D, n_splits);
   char* ws = static_cast<char*>(partials);
   p.part_m = reinterpret_cast<float*>(ws + w.m);
   p.part_l = reinterpret_cast<float*>(ws + w.l);
@@ -728,11 +1072,13 @@ static int decode_entry(DecodeParams& p, void* partials, int32_t* counters, int6
   p.H_kv = (int32_t)H_kv;
   p.G = (int32_t)G;
   p.page_size = (int32_t)page_size;
-  p.n_splits = (int32_t)n_splits;
+  p.n_splits = kPlanned ? 0 : (int32_t)n_splits;
+  p.n_wg = kPlanned ? (int32_t)n_splits : 0;
   p.scale_log2 = kLog2e / __builtin_sqrtf((float)D);
   p.err = err;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return D == 64 ? launch_decode<64, kAppend, kRope>(p, s) : launch_decode<128, kAppend, kRope>(p, s);
+  return D == 64 ? launch_decode<64, kAppend, kRope, kPlanned>(p, s)
+                 : launch_decode<128, kAppend, kRope, kPlanned>(p, s);
 }
 
 }  // namespace cie
@@ -845,6 +1191,156 @@ extern "C" int cie_paged_decode_qkv_rope(
   return decode_entry<true, true>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages,
                                   pool_page_stride, pool_head_stride, bt_stride, bt_width,
                                   n_slots, n_splits, err, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Planned decode: cie_paged_decode_plan once per decode step, then one
+// planned launch per layer.
+extern "C" int64_t cie_paged_decode_plan_workgroups(int64_t B, int64_t H_kv, int64_t n_splits) {
+  if (B <= 0 || H_kv <= 0 || n_splits < 0 || n_splits > kMaxSplits) return -1;
+  if (n_splits > 0) return B * H_kv * n_splits;
+  // the library's default: about one workgroup per CU (one resident round),
+  // at least one and at most kMaxSplits per (sequence, kv head)
+  int64_t per_head = (device_cus() + H_kv - 1) / H_kv;
+  if (per_head < B) per_head = B;
+  if (per_head > B * kMaxSplits) per_head = B * kMaxSplits;
+  return H_kv * per_head;
+}
+
+extern "C" int64_t cie_paged_decode_plan_bytes(int64_t n_workgroups) {
+  if (n_workgroups <= 0) return -1;
+  return n_workgroups * (kPlanDescWords + kPlanWaves * kWave) * (int64_t)sizeof(int32_t);
+}
+
+extern "C" int64_t cie_paged_decode_planned_partials_bytes(int64_t n_workgroups, int64_t H_q,
+                                                           int64_t H_kv, int64_t D) {
+  if (n_workgroups <= 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 || D <= 0) return -1;
+  return part_layout_rows(n_workgroups * (H_q / H_kv), D).total;
+}
+
+extern "C" int cie_paged_decode_plan(void* plan, const int64_t* lens, const int64_t* slot_ids,
+                                     const int64_t* block_table, int64_t B, int64_t H_kv,
+                                     int64_t page_size, int64_t n_pages, int64_t bt_stride,
+                                     int64_t bt_width, int64_t n_slots, int64_t append,
+                                     int64_t n_workgroups, int32_t* err, void* stream) {
+  if (B < 0 || H_kv <= 0 || page_size <= 0 || n_pages <= 0 || bt_width <= 0 ||
+      bt_stride < bt_width || n_slots <= 0 || (append != 0 && append != 1))
+    return CIE_EINVAL;
+  if (B == 0) return CIE_OK;
+  if (!plan || !lens || !slot_ids || !block_table) return CIE_EINVAL;
+  if (n_workgroups < B * H_kv || n_workgroups % H_kv != 0 || n_workgroups > B * H_kv * kMaxSplits)
+    return CIE_EINVAL;
+  if (B > kPlanMaxSeqs || page_size % 16 != 0 || n_workgroups > 0x7fffffff ||
+      bt_width * page_size > 0x7fffffff)
+    return CIE_EUNSUPPORTED;
+  if (reinterpret_cast<uintptr_t>(plan) & 15) return CIE_EINVAL;
+  PlanParams q{};
+  q.plan = static_cast<int32_t*>(plan);
+  q.lens = lens;
+  q.slot_ids = slot_ids;
+  q.block_table = block_table;
+  q.bt_stride = bt_stride;
+  q.n_pages = n_pages;
+  q.B = (int32_t)B;
+  q.H_kv = (int32_t)H_kv;
+  q.page_size = (int32_t)page_size;
+  q.bt_width = (int32_t)bt_width;
+  q.n_slots = (int32_t)(n_slots > 0x7fffffff ? 0x7fffffff : n_slots);
+  q.n_wg = (int32_t)n_workgroups;
+  q.append = (int32_t)append;
+  q.err = err;
+  hipLaunchKernelGGL(decode_plan_kernel, dim3((unsigned)n_workgroups), dim3(kPlanThreads), 0,
+                     static_cast<hipStream_t>(stream), q);
+  return (int)hipGetLastError();
+}
+
+extern "C" int cie_paged_decode_planned(void* o, const void* q, const void* k_pool,
+                                        const void* v_pool, const int32_t* plan,
+                                        const int64_t* block_table, void* partials,
+                                        int32_t* counters, int64_t B, int64_t H_q, int64_t H_kv,
+                                        int64_t D, int64_t page_size, int64_t n_pages,
+                                        int64_t pool_page_stride, int64_t pool_head_stride,
+                                        int64_t bt_stride, int64_t bt_width, int64_t n_workgroups,
+                                        int32_t* err, void* stream) {
+  DecodeParams p{};
+  p.o = static_cast<f16*>(o);
+  p.q = static_cast<const f16*>(q);
+  p.k_pool = const_cast<f16*>(static_cast<const f16*>(k_pool));
+  p.v_pool = const_cast<f16*>(static_cast<const f16*>(v_pool));
+  p.q_row_stride = H_q * D;
+  p.plan = plan;
+  p.block_table = block_table;
+  return decode_entry<false, false, true>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages,
+                                          pool_page_stride, pool_head_stride, bt_stride, bt_width,
+                                          0, n_workgroups, err, stream);
+}
+
+extern "C" int cie_paged_decode_append_planned(
+    void* o, const void* q, void* k_pool, void* v_pool, const void* k_new, const void* v_new,
+    int64_t k_tok_stride, int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+    const int32_t* plan, const int64_t* block_table, void* partials, int32_t* counters, int64_t B,
+    int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size, int64_t n_pages,
+    int64_t pool_page_stride, int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
+    int64_t n_workgroups, int32_t* err, void* stream) {
+  if (B > 0 && (!k_new || !v_new)) return CIE_EINVAL;
+  if (((reinterpret_cast<uintptr_t>(k_new) | reinterpret_cast<uintptr_t>(v_new)) & 15) ||
+      k_tok_stride % 8 != 0 || k_head_stride % 8 != 0 || v_tok_stride % 8 != 0 ||
+      v_head_stride % 8 != 0)
+    return CIE_EINVAL;
+  DecodeParams p{};
+  p.o = static_cast<f16*>(o);
+  p.q = static_cast<const f16*>(q);
+  p.k_pool = static_cast<f16*>(k_pool);
+  p.v_pool = static_cast<f16*>(v_pool);
+  p.k_new = static_cast<const f16*>(k_new);
+  p.v_new = static_cast<const f16*>(v_new);
+  p.k_tok_stride = k_tok_stride;
+  p.k_head_stride = k_head_stride;
+  p.v_tok_stride = v_tok_stride;
+  p.v_head_stride = v_head_stride;
+  p.q_row_stride = H_q * D;
+  p.plan = plan;
+  p.block_table = block_table;
+  return decode_entry<true, false, true>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages,
+                                         pool_page_stride, pool_head_stride, bt_stride, bt_width, 0,
+                                         n_workgroups, err, stream);
+}
+
+extern "C" int cie_paged_decode_qkv_rope_planned(
+    void* o, const void* qkv, int64_t qkv_row_stride, const void* cos, const void* sin,
+    int64_t cs_row_stride, void* k_pool, void* v_pool, const int32_t* plan,
+    const int64_t* block_table, void* partials, int32_t* counters, int64_t B, int64_t H_q,
+    int64_t H_kv, int64_t D, int64_t page_size, int64_t n_pages, int64_t pool_page_stride,
+    int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width, int64_t n_workgroups,
+    int32_t* err, void* stream) {
+  if (B < 0 || H_q <= 0 || H_kv <= 0 || D <= 0) return CIE_EINVAL;
+  if (B > 0 && (!qkv || !cos || !sin)) return CIE_EINVAL;
+  if (((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(cos) |
+        reinterpret_cast<uintptr_t>(sin)) & 15) ||
+      qkv_row_stride % 8 != 0 || cs_row_stride % 8 != 0 ||
+      qkv_row_stride < (H_q + 2 * H_kv) * D || cs_row_stride < D)
+    return CIE_EINVAL;
+  const f16* base = static_cast<const f16*>(qkv);
+  DecodeParams p{};
+  p.o = static_cast<f16*>(o);
+  p.q = base;
+  p.q_row_stride = qkv_row_stride;
+  p.cos = static_cast<const f16*>(cos);
+  p.sin = static_cast<const f16*>(sin);
+  p.cs_stride = cs_row_stride;
+  p.k_pool = static_cast<f16*>(k_pool);
+  p.v_pool = static_cast<f16*>(v_pool);
+  p.k_new = base + H_q * D;
+  p.v_new = base + (H_q + H_kv) * D;
+  p.k_tok_stride = qkv_row_stride;
+  p.k_head_stride = D;
+  p.v_tok_stride = qkv_row_stride;
+  p.v_head_stride = D;
+  p.plan = plan;
+  p.block_table = block_table;
+  return decode_entry<true, true, true>(p, partials, counters, B, H_q, H_kv, D, page_size, n_pages,
+                                        pool_page_stride, pool_head_stride, bt_stride, bt_width, 0,
+                                        n_workgroups, err, stream);
 }
 
 // ---------------------------------------------------------------------------

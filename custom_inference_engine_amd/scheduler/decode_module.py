@@ -10,7 +10,11 @@ is read inside the graph: the input token of sequence b is
 ``kv_cache.last_generated[slot_b]`` and its position is ``kv_cache.lens[slot_b]``
 (two gathers recorded in the graph), the attention layers append and attend
 through the fused decode kernel, ``decode_advance`` moves the lengths on, and
-the LM head produces the bucket's logits.  A step is therefore: write the slot
+the LM head produces the bucket's logits.  The step's first launch is the
+decode plan (``inference::gqa_decode_plan``): every layer's decode reads the
+same slots, lengths and block-table rows, so their split counts (balanced by
+length) and page ids are worked out once and each layer's launch starts one
+memory round trip sooner.  A step is therefore: write the slot
 ids into a pinned block, one asynchronous copy, one graph replay, then the
 argmax and the ``last_generated`` update (kept out of the graph: argmax over a
 151,936-wide vocabulary is a multi-block library reduction, and such library
@@ -24,6 +28,7 @@ from __future__ import annotations
 
 import torch
 
+from ..attn.core import gqa_decode_plan_op
 from ..attn.metadata import AttentionMetadata
 from ..graphs import StepGraph, StepInputs
 
@@ -50,6 +55,10 @@ class DecodeModule:
 
     def _step(self) -> torch.Tensor:
         kv = self.kv_cache
+        # one plan for every layer's decode launch (their slots, lengths and
+        # block-table rows are the step's): splits balanced by length, page
+        # ids resolved once
+        self.metadata.decode_plan = gqa_decode_plan_op(kv.keys[0], kv.lens, self.slots, kv.block_table)
         torch.index_select(kv.last_generated, 0, self.slots, out=self.tokens)
         torch.index_select(kv.lens, 0, self.slots, out=self.positions)
         hidden = self.model.model(input_ids=self.tokens[None], position_ids=self.positions[None],

@@ -155,6 +155,78 @@ int cie_paged_decode_append(void* o, const void* q, void* k_pool, void* v_pool,
                             void* stream);
 
 /*
+ * Planned decode.  The slot ids, lengths and block-table rows a decode step
+ * reads are the same for every layer of the step (KVStorage advances the
+ * lengths after the last layer), so a step can make a plan once and run each
+ * layer's decode from it:
+ *   cie_paged_decode_plan       once per step: each sequence's attended
+ *                               length (append = 1: lens is (n_slots,) prior
+ *                               lengths, attended = lens[slot] + 1, as
+ *                               cie_paged_decode_append; append = 0: lens is
+ *                               (B,) attended lengths, as cie_paged_decode),
+ *                               its splits (balanced by length over the
+ *                               n_workgroups of the grid) and each workgroup's
+ *                               page ids, into `plan`
+ *                               (cie_paged_decode_plan_bytes(n_workgroups)
+ *                               bytes, 16-byte aligned, any contents).  Index
+ *                               errors are reported here (CIE_ERRBIT_*).
+ *   cie_paged_decode_planned,   per layer: the same results as
+ *   cie_paged_decode_append_planned,   cie_paged_decode / _append / _qkv_rope
+ *   cie_paged_decode_qkv_rope_planned  on the plan's sequences, but the
+ *                               launch reads one descriptor and its page ids
+ *                               instead of the slot id, then the block table
+ *                               and the length: one memory round trip less
+ *                               before its first K/V loads.
+ * The plan must be made with the same append mode, block table and lengths
+ * as the layers' calls, and n_workgroups must be the same for all of them.
+ * n_workgroups = cie_paged_decode_plan_workgroups(B, H_kv, n_splits):
+ * B * H_kv * n_splits, or with n_splits = 0 the library's default (about
+ * one workgroup per CU, at least one per (sequence, kv head)); it must lie
+ * in [B * H_kv, B * H_kv * cie_paged_decode_max_splits()] and be a multiple
+ * of H_kv.  Equal lengths give every (sequence, kv head) n_workgroups /
+ * (B * H_kv) splits; unequal ones give longer sequences more.  partials:
+ * cie_paged_decode_planned_partials_bytes(n_workgroups, H_q, H_kv, D);
+ * counters: 2 * B * H_kv words as for cie_paged_decode.  B <= 1024.
+ * Replaces decode_gqa_attention (attn/core.py:13-66) and its grid
+ * (P, H_kv, B) (attn/core.py:37) for every layer of a decode step.
+ */
+int64_t cie_paged_decode_plan_workgroups(int64_t B, int64_t H_kv, int64_t n_splits);
+int64_t cie_paged_decode_plan_bytes(int64_t n_workgroups);
+int64_t cie_paged_decode_planned_partials_bytes(int64_t n_workgroups, int64_t H_q, int64_t H_kv,
+                                                int64_t D);
+int cie_paged_decode_plan(void* plan, const int64_t* lens, const int64_t* slot_ids,
+                          const int64_t* block_table, int64_t B, int64_t H_kv,
+                          int64_t page_size, int64_t n_pages, int64_t bt_stride,
+                          int64_t bt_width, int64_t n_slots, int64_t append,
+                          int64_t n_workgroups, int32_t* err, void* stream);
+int cie_paged_decode_planned(void* o, const void* q, const void* k_pool, const void* v_pool,
+                             const int32_t* plan, const int64_t* block_table, void* partials,
+                             int32_t* counters, int64_t B, int64_t H_q, int64_t H_kv, int64_t D,
+                             int64_t page_size, int64_t n_pages, int64_t pool_page_stride,
+                             int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
+                             int64_t n_workgroups, int32_t* err, void* stream);
+int cie_paged_decode_append_planned(void* o, const void* q, void* k_pool, void* v_pool,
+                                    const void* k_new, const void* v_new,
+                                    int64_t k_tok_stride, int64_t k_head_stride,
+                                    int64_t v_tok_stride, int64_t v_head_stride,
+                                    const int32_t* plan, const int64_t* block_table,
+                                    void* partials, int32_t* counters,
+                                    int64_t B, int64_t H_q, int64_t H_kv, int64_t D,
+                                    int64_t page_size, int64_t n_pages,
+                                    int64_t pool_page_stride, int64_t pool_head_stride,
+                                    int64_t bt_stride, int64_t bt_width, int64_t n_workgroups,
+                                    int32_t* err, void* stream);
+int cie_paged_decode_qkv_rope_planned(void* o, const void* qkv, int64_t qkv_row_stride,
+                                      const void* cos, const void* sin, int64_t cs_row_stride,
+                                      void* k_pool, void* v_pool, const int32_t* plan,
+                                      const int64_t* block_table, void* partials,
+                                      int32_t* counters, int64_t B, int64_t H_q, int64_t H_kv,
+                                      int64_t D, int64_t page_size, int64_t n_pages,
+                                      int64_t pool_page_stride, int64_t pool_head_stride,
+                                      int64_t bt_stride, int64_t bt_width, int64_t n_workgroups,
+                                      int32_t* err, void* stream);
+
+/*
  * Allocation-free form of cie_paged_decode_append.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * hipGraph stream capture, tight serving loops, harnesses that forbid

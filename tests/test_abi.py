@@ -193,3 +193,23 @@ def test_noalloc_limit_rejects_impossible_arguments(native_lib):
     assert lib.cie_paged_decode_noalloc_limit(14, 2, 64, lib.cie_paged_decode_max_splits() + 1) == -1
     assert lib.cie_paged_decode_noalloc_limit(14, 3, 64, 4) == -1  # H_q not a multiple of H_kv
     assert lib.cie_paged_decode_noalloc_limit(14, 2, 64, 0) == -1
+
+
+def test_plan_rejects_what_it_cannot_hold(native_lib):
+    """cie_paged_decode_plan checks its sizes on the host (fake addresses, never read)."""
+    lib = native_lib
+    # more sequences than one plan holds
+    assert lib.cie_paged_decode_plan(16, 16, 16, 16, 1025, 2, 16, 64, 64, 64, 2000, 1,
+                                     lib.cie_paged_decode_plan_workgroups(1025, 2, 1), None, None) == -2
+    # fewer workgroups than (sequence, kv head) groups; a grid not a multiple of H_kv
+    assert lib.cie_paged_decode_plan(16, 16, 16, 16, 4, 2, 16, 64, 64, 64, 10, 1, 6, None, None) == -1
+    assert lib.cie_paged_decode_plan(16, 16, 16, 16, 4, 2, 16, 64, 64, 64, 10, 1, 9, None, None) == -1
+    assert lib.cie_paged_decode_plan(16, 16, 16, 16, 0, 2, 16, 64, 64, 64, 10, 1, 8, None, None) == 0
+    # the planned launch wants a plan and a grid of at least one workgroup per group
+    assert lib.cie_paged_decode_planned(16, 16, 16, 16, None, 16, 16, 16, 4, 14, 2, 64, 16, 64, 2048,
+                                        1024, 64, 64, 8, None, None) == -1
+    assert lib.cie_paged_decode_planned(16, 16, 16, 16, 16, 16, 16, 16, 4, 14, 2, 64, 16, 64, 2048,
+                                        1024, 64, 64, 6, None, None) == -1
+    assert lib.cie_paged_decode_plan_workgroups(4, 2, 65) == -1
+    assert lib.cie_paged_decode_plan_workgroups(4, 2, 16) == 128
+    assert lib.cie_paged_decode_plan_bytes(256) == 256 * (8 + 4 * 64) * 4
