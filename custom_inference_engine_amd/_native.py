@@ -100,13 +100,13 @@ _SIGNATURES = {
     "cie_mixed_counters": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "cie_mixed_attention": (
         ctypes.c_int,
-        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_ptr, _c_ptr, _c_i64,
-         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64p, _c_i64p, _c_i64p, _c_i64p, _c_ptr, _c_i64, _c_ptr,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_ptr, _c_ptr],
     ),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

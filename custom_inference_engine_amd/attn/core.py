@@ -435,12 +435,16 @@ def _as_rows(x: torch.Tensor, h_kv: int, d: int) -> torch.Tensor:
 
 
 def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids, block_table,
-                        BLOCK_M=16, BLOCK_N=64, num_warps=4, wrap=None, err=None, counters=None):
+                        BLOCK_M=16, BLOCK_N=64, num_warps=4, wrap=None, err=None, counters=None,
+                        partials_bytes=None):
     """Varlen causal GQA attention over the paged pool (chunked prefill + decode).
 
     q: (1, total_T, H_q, D) fp16 contiguous; cu_seqlens (B+1,); kv_lens (B,) =
     prior lengths; row i of sequence b attends keys [0, kv_lens[b] + i].
     Rows outside every sequence are left as ``torch.empty_like`` leaves them.
+    ``partials_bytes`` is the budget of split-chunk partial state (default
+    ``cie_mixed_partials_bytes``: 2 rows per token and q head); sequences
+    whose split tiles do not fit it run unsplit, with the same results.
     """
     total_T, H_q, D = q.shape[1:]
     N_PAGES, H_kv, PAGE_SIZE, _ = k.shape
@@ -459,7 +463,10 @@ def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids,
     o = torch.empty_like(q)
     if B == 0 or total_T == 0 or int(max_seqlen) == 0:
         return o
-    partials = torch.empty(lib.cie_mixed_partials_bytes(total_T, H_q, D), dtype=torch.uint8, device=dev)
+    if partials_bytes is None:
+        partials_bytes = lib.cie_mixed_partials_bytes(total_T, H_q, D)
+    _require(partials_bytes >= 0, "partials_bytes must be >= 0")
+    partials = torch.empty(partials_bytes, dtype=torch.uint8, device=dev)
     n_ctr = lib.cie_mixed_counters(B, H_kv, int(max_seqlen))
     if counters is None:
         counters = split_counters(dev, n_ctr)
@@ -468,7 +475,8 @@ def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids,
         lib.cie_mixed_attention(
             o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
             cu_seqlens.data_ptr(), kv_lens.data_ptr(), slot_ids.data_ptr(), block_table.data_ptr(),
-            partials.data_ptr(), counters.data_ptr(), B, total_T, int(max_seqlen), H_q, H_kv, D, PAGE_SIZE, N_PAGES,
+            _native.ptr(partials) if partials_bytes else None, partials_bytes, counters.data_ptr(),
+            B, total_T, int(max_seqlen), H_q, H_kv, D, PAGE_SIZE, N_PAGES,
             k.stride(0), k.stride(1), block_table.stride(0), block_table.shape[1],
             block_table.shape[0], _native.ptr(err), _native.stream_handle(dev),
         ),

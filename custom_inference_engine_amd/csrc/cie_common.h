@@ -27,6 +27,20 @@ __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
+// Inclusive prefix sum over the wave's 64 lanes, by DPP (no LDS): shifts
+// by 1, 2, 4 and 8 lanes within each row of 16 (lanes shifted in from before
+// the row read 0), then lane 15's row total added into rows 1 and 3 and
+// lane 31's running total into rows 2 and 3.  Every lane must be active.
+__device__ __forceinline__ int wave_inclusive_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2 and 3
+  return v;
+}
+
 // Lane exchange l <-> l^m (ds_bpermute under the hood).
 __device__ __forceinline__ float lane_xor(float x, int m) {
   return __shfl_xor(x, m, kWave);

@@ -25,7 +25,9 @@
 // item writes o directly.  Otherwise each chunk writes its partial (m, l, acc) per column
 // with device-coherent stores and the last chunk to arrive (counter per
 // tile and column group) merges them with log-sum-exp, writes o and resets
-// the counter.  The reference instead walks a tile's whole prefix with one
+// the counter.  Partials are packed per launch: only split tiles have rows,
+// sequence by sequence, within a budget the caller's buffer sets; a
+// sequence past it runs unsplit (see the tile runs below).  The reference instead walks a tile's whole prefix with one
 // program and pads every L = 1 sequence to a 16-row tile
 // (prefill_attention.py:49-50, 93).
 #include "attn_engine.h"
@@ -49,6 +51,9 @@ namespace cie {
 //   CIE_MIXED_SHORT_KTILES a sequence whose longest tile has at most this
 //                          many 16-key tiles uses column groups of half
 //                          CIE_MIXED_CG (0: never)
+//   CIE_MIXED_LONG_KTILES  the same for a sequence whose longest tile has at
+//                          least this many (0: never; 96 and 128 measured
+//                          slower at config 3: 24.6 against 21.7 us)
 #ifndef CIE_MIXED_WAVES
 #define CIE_MIXED_WAVES 4
 #endif
@@ -85,10 +90,17 @@ namespace cie {
 #ifndef CIE_MIXED_SHORT_KTILES
 #define CIE_MIXED_SHORT_KTILES 32
 #endif
+#ifndef CIE_MIXED_LONG_KTILES
+#define CIE_MIXED_LONG_KTILES 0
+#endif
 
 constexpr int kWavePairs = CIE_MIXED_WAVE_PAIRS;
 constexpr int kMaxChunks = 16;    // workgroups per (tile, column group) at most
 constexpr int kMaxColGroups = 8;  // column groups per tile at most (<= 8 column tiles)
+// Partial rows a launch uses at most, whatever the buffer: with each
+// sequence's rows clamped to the budget + 1, the plan's prefix over kMaxSeqs
+// sequences stays below 2^31.
+constexpr int64_t kMaxPartRows = (1 << 21) - 64;
 
 
 // Wavefronts per workgroup, column tiles per work item (registers: 16*NT
@@ -136,9 +148,10 @@ struct MixedParams {
   const int64_t* kv_lens;
   const int64_t* slot_ids;
   const int64_t* block_table;
-  float* part_m;  // [total_T][H_q][kMaxChunks]
-  float* part_l;
-  float* part_acc;  // [total_T][H_q][kMaxChunks][D]
+  float* part_m;    // [part_cap] split-chunk partial rows (m): packed, see the tile runs
+  float* part_l;    // [part_cap]
+  float* part_acc;  // [part_cap][D]
+  int64_t part_cap;  // partial rows the caller's buffer holds (<= kMaxPartRows)
   int32_t* counters;  // 2 x [B][H_kv][n_qtiles][kMaxColGroups]: arrival words, then stale words
   int64_t pool_page_stride, pool_head_stride, bt_stride, n_pages, total_T;
   int32_t bt_width, n_slots, B, H_q, H_kv, G, page_size, n_qtiles;
@@ -153,10 +166,13 @@ struct SeqInfo {
   int64_t slot;
   int L;  // query rows
   int c;  // prior kv length
+  // first partial row of the sequence's split tiles, or -1: its tiles are
+  // not split (the batch's partial rows would exceed the caller's buffer)
+  int pbase;
 };
 
 __device__ __forceinline__ SeqInfo seq_info(const MixedParams& p, int b) {
-  SeqInfo s{0, 0, 0, 0};
+  SeqInfo s{0, 0, 0, 0, 0};
   const int64_t t0 = p.cu_seqlens[b];
   const int64_t t1 = p.cu_seqlens[b + 1];
   const int64_t slot = p.slot_ids[b];
@@ -179,6 +195,7 @@ __device__ __forceinline__ SeqInfo seq_info(const MixedParams& p, int b) {
 
 struct TilePlan {
   int row0, rows, n_combos, n_ctiles, cg, n_groups, key_end, n_ktiles, n_pairs, n_chunks;
+  int pblk;  // first partial row of a split tile's block (set per work item: part_region)
 };
 
 // Column tiles per group for every tile of a sequence: CG, or CG / 2 when
@@ -190,8 +207,11 @@ struct TilePlan {
 // lookup and the item agree.
 template <int CG>
 __device__ __forceinline__ int seq_cg(const SeqInfo& s) {
-  if constexpr (CG < 4 || CIE_MIXED_SHORT_KTILES <= 0) return CG;
-  return ((s.c + s.L + 15) >> 4) <= CIE_MIXED_SHORT_KTILES ? CG / 2 : CG;
+  if constexpr (CG < 4) return CG;
+  const int kt = (s.c + s.L + 15) >> 4;
+  if (CIE_MIXED_SHORT_KTILES > 0 && kt <= CIE_MIXED_SHORT_KTILES) return CG / 2;
+  if (CIE_MIXED_LONG_KTILES > 0 && kt >= CIE_MIXED_LONG_KTILES) return CG / 2;
+  return CG;
 }
 
 // Column groups of n column tiles at cg per group (cg = CG or CG / 2: both
@@ -221,7 +241,8 @@ __device__ __forceinline__ TilePlan tile_plan(int qt, const SeqInfo& s, int G) {
   constexpr int kPerWide = W * kWavePairs;
   const int chunks = t.n_ctiles == 1 ? (t.n_pairs + kPerNarrow - 1) / kPerNarrow
                                      : (t.n_pairs + kPerWide - 1) / kPerWide;
-  t.n_chunks = max(1, min(kMaxChunks, chunks));
+  t.n_chunks = s.pbase < 0 ? 1 : max(1, min(kMaxChunks, chunks));
+  t.pblk = 0;
   return t;
 }
 
@@ -322,23 +343,22 @@ __shared__ uint64_t sm_mixed_trace[16];
   } while (0)
 #endif
 
-// Where a tile's partial state lives: rows r = column_off(...) of the tile
-// (relative to row (t0 + row0) * H_q), chunk k.
+// Where a split tile's partial state lives: row column_off * n_chunks +
+// chunk of the tile's block, which starts at row tp.pblk (the layout is
+// described with the tile runs below).
 struct PartRegion {
-  __amdgpu_buffer_rsrc_t acc;  // over the tile's 16 * H_q * kMaxChunks * D floats
-  float* m;                    // tile-relative row 0 of part_m
+  __amdgpu_buffer_rsrc_t acc;  // over the tile's rows * H_q * n_chunks * D floats
+  float* m;                    // the tile block's row 0 of part_m
   float* l;
 };
 
 template <int D>
-__device__ __forceinline__ PartRegion part_region(const MixedParams& p, const SeqInfo& s,
-                                                  const TilePlan& tp) {
-  const int64_t row0 = (s.t0 + tp.row0) * p.H_q;
+__device__ __forceinline__ PartRegion part_region(const MixedParams& p, const TilePlan& tp) {
   PartRegion r;
-  r.acc = coherent_rsrc(p.part_acc + row0 * kMaxChunks * D,
-                        (uint32_t)(16 * p.H_q * kMaxChunks * D * sizeof(float)));
-  r.m = p.part_m + row0 * kMaxChunks;
-  r.l = p.part_l + row0 * kMaxChunks;
+  r.acc = coherent_rsrc(p.part_acc + (int64_t)tp.pblk * D,
+                        (uint32_t)(tp.rows * p.H_q * tp.n_chunks * D * sizeof(float)));
+  r.m = p.part_m + tp.pblk;
+  r.l = p.part_l + tp.pblk;
   return r;
 }
 
@@ -419,7 +439,7 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
   r16 = lane & 15;
   grp = lane >> 4;
   const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
-  const PartRegion pr = part_region<D>(p, s, tp);
+  const PartRegion pr = part_region<D>(p, tp);  // (used only if tp.n_chunks > 1)
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     if (c == wave) continue;  // wave c keeps its own state in registers
@@ -482,7 +502,7 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
             *reinterpret_cast<f16x8*>(p.o + (tile_row0 + off) * D + d0 + 8 * h) = v;
           }
         } else {
-          const int prow = off * kMaxChunks + chunk;
+          const int prow = off * tp.n_chunks + chunk;
 #pragma unroll
           for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -516,7 +536,7 @@ __device__ __forceinline__ void merge_group(const MixedParams& p, const SeqInfo&
   const int K = tp.n_chunks;
   const int n_units = n_cols * (D / 4);
   const int64_t tile_row0 = (s.t0 + tp.row0) * p.H_q;
-  const PartRegion pr = part_region<D>(p, s, tp);
+  const PartRegion pr = part_region<D>(p, tp);
   const int tid = opaque((int)threadIdx.x);
   int off[kUnits], d4[kUnits];
   bool live[kUnits];
@@ -540,7 +560,7 @@ __device__ __forceinline__ void merge_group(const MixedParams& p, const SeqInfo&
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
       for (int c = 0; c < kGroup; ++c) {
-        const int prow = off[u] * kMaxChunks + k0 + c;
+        const int prow = off[u] * K + k0 + c;
         if (live[u] && k0 + c < K) {
           mk[u][c] = agent_load(pr.m + prow);
           lk[u][c] = agent_load(pr.l + prow);
@@ -583,11 +603,12 @@ constexpr int kMaxSeqs = 1024;  // sequences a launch can plan (LDS plan tables)
 constexpr int kRankSeqs = 64;   // batches up to this size deal their items heaviest first
 static_assert(kRankSeqs == kWave, "a batch small enough to rank is planned by one wave");
 
-// Bytes of the kernel's dynamic LDS: the plan tables of B sequences — t0 as
-// int64; slot, rows, prior, the order and the item prefix (B + 1 entries)
-// as int32.
+// Bytes of the kernel's dynamic LDS: the plan tables of B sequences — t0
+// and the partial base as an int2 (one read); slot, rows, prior, the order
+// and the item prefix (B + 1 entries) as int32.  (t0 < total_T < 2^31: the
+// launch bounds total_T * kMaxColGroups * kMaxChunks by 2^31.)
 constexpr size_t mixed_plan_lds(int B) {
-  return (size_t)B * sizeof(int64_t) + (size_t)(4 * B + (B + 1)) * sizeof(int);
+  return (size_t)B * sizeof(int2) + (size_t)(4 * B + (B + 1)) * sizeof(int);
 }
 
 // LDS one workgroup may allocate on gfx950.
@@ -608,6 +629,7 @@ struct SeqTiles {
   bool partial;  // tile n_tiles - 1 has fewer than 16 rows
   int ng_full;   // column groups of a full tile
   bool full_narrow;  // a full tile is one column tile (G = 1): narrow chunks
+  bool split;        // the sequence has partial rows (pbase >= 0): tiles may chunk
 };
 
 template <int CG, int W>
@@ -619,11 +641,13 @@ __device__ __forceinline__ SeqTiles seq_tiles(const SeqInfo& s, int n_qtiles, in
   t.partial = t.n_tiles > t.n_full;
   t.ng_full = n_col_groups<CG>(G, seq_cg<CG>(s));
   t.full_narrow = G <= 1;
+  t.split = s.pbase >= 0;
   return t;
 }
 
 // Visit the runs of full tiles [0, n) with equal chunk counts (Q key tiles a
 // chunk), from the top tile down: f(t_lo, t_hi, k) returns true to stop.
+// (A sequence that may not split has one run, of one chunk: full_runs.)
 template <int Q, class F>
 __device__ __forceinline__ void chunk_runs(int n, int c16, F f) {
   for (int t_hi = n - 1; t_hi >= 0;) {
@@ -646,17 +670,46 @@ constexpr int narrow_chunk_ktiles() {
 
 template <int W, class F>
 __device__ __forceinline__ void full_runs(const SeqTiles& st, F f) {
-  if (st.full_narrow) chunk_runs<narrow_chunk_ktiles<W>()>(st.n_full, st.c16, f);
+  if (!st.split) {
+    if (st.n_full > 0) f(0, st.n_full - 1, 1);
+  } else if (st.full_narrow) chunk_runs<narrow_chunk_ktiles<W>()>(st.n_full, st.c16, f);
   else chunk_runs<wide_chunk_ktiles<W>()>(st.n_full, st.c16, f);
 }
 
-// Items of one sequence, and its weight: the key tiles of its heaviest
-// chunk (the top tile's), the order in which batches of up to kRankSeqs
-// sequences deal their items.
+// The partials of a launch are packed: only split tiles (two chunks or more)
+// have any.  Sequence b's split tiles own rows [pbase_b, pbase_b + P_b) of
+// the partial arrays — its full tiles in tile order, then its partial last
+// tile — and tile t's block holds rows_t * H_q * chunks_t rows: row
+// column_off * chunks_t + chunk, column_off = row * H_q + g * G + head (every
+// kv head's columns).  pbase_b is the prefix of P_b over the batch in
+// sequence order; a sequence whose block would end past the caller's buffer
+// is not split at all (pbase = -1: one chunk per tile, no partials), so a
+// launch never needs more than the buffer it was given, and parity does not
+// depend on the budget (an unsplit tile is the same attention, later).
+
+// First row of query tile qt's block within its sequence's partial rows.
 template <int CG, int W>
-__device__ __forceinline__ int seq_items(const SeqInfo& s, const SeqTiles& st, int G, int& weight) {
+__device__ __forceinline__ int tile_partial_off(const SeqTiles& st, int qt, int H_q) {
+  // full tiles below qt (all full tiles, for the partial last tile)
+  const int below = (st.partial && qt == st.n_tiles - 1) ? st.n_full : qt;
+  int off = 0;
+  full_runs<W>(st, [&](int lo, int hi, int k) {
+    const int top = min(hi, below - 1);
+    if (k > 1 && top >= lo) off += (top - lo + 1) * 16 * H_q * k;
+    return false;
+  });
+  return off;
+}
+
+// Items of one sequence; its weight: the key tiles of its heaviest chunk
+// (the top tile's), the order in which batches of up to kRankSeqs sequences
+// deal their items; and its partial rows (P_b above: 0 if it does not split).
+template <int CG, int W>
+__device__ __forceinline__ int seq_items(const SeqInfo& s, const SeqTiles& st, int G, int H_q,
+                                         int& weight, int& prows) {
   int n = 0;
   weight = 0;
+  prows = 0;
   if (st.n_tiles <= 0) return 0;
   const TilePlan top = tile_plan<CG, W>(st.n_tiles - 1, s, G);
   weight = (top.n_ktiles + top.n_chunks - 1) / top.n_chunks;
@@ -664,10 +717,14 @@ __device__ __forceinline__ int seq_items(const SeqInfo& s, const SeqTiles& st, i
     if (CIE_MIXED_NARROW_ORDER == 1) weight = 0;
     if (CIE_MIXED_NARROW_ORDER == 2) weight += 1 << 24;
   }
-  if (st.partial) n += top.n_groups * top.n_chunks;
+  if (st.partial) {
+    n += top.n_groups * top.n_chunks;
+    if (top.n_chunks > 1) prows += top.rows * H_q * top.n_chunks;
+  }
   const int ng = st.ng_full;
   full_runs<W>(st, [&](int lo, int hi, int k) {
     n += (hi - lo + 1) * ng * k;
+    if (k > 1) prows += (hi - lo + 1) * 16 * H_q * k;
     return false;
   });
   return n;
@@ -722,9 +779,12 @@ __device__ __forceinline__ int2 block_scan2(int2 v, int2* sm, int span) {
 // prefix[0] <= x): i + 1 such entries, counted 64 per LDS read with a ballot.
 __device__ __forceinline__ int prefix_search(const int* prefix, int n, int x) {
   int n_le = 0;
+  // (the lane's address derived afresh: hoisted out of the item loop, it
+  // would hold a register through every key loop)
+  const int* const mine = prefix + (opaque((int)threadIdx.x) & (kWave - 1));
   for (int i0 = 0; i0 < n; i0 += kWave) {
     const int i = i0 + (int)(threadIdx.x & (kWave - 1));
-    const uint64_t le = __ballot(i < n && prefix[i] <= x);
+    const uint64_t le = __ballot(i < n && mine[i0] <= x);
     n_le += __popcll(le);
     if (~le != 0) break;
   }
@@ -744,7 +804,13 @@ __device__ __forceinline__ void process_item(const MixedParams& p, const SeqInfo
   const int wave = uniform(tid / kWave);
   const int r16 = lane & 15;
   const int grp = lane >> 4;
-  const TilePlan tp = tile_plan<CG, W>(qt, s, p.G);
+  TilePlan tp = tile_plan<CG, W>(qt, s, p.G);
+  // the block's base, taken once here, where the key loop's registers are
+  // not yet live (after the loop, the run walk it takes spills scalars)
+  if (tp.n_chunks > 1)
+    tp.pblk = s.L <= 16 ? s.pbase  // one tile
+                        : uniform(s.pbase + tile_partial_off<CG, W>(seq_tiles<CG, W>(s, p.n_qtiles, p.G),
+                                                                    qt, p.H_q));
   const int gi = j / tp.n_chunks;
   const int chunk = j - gi * tp.n_chunks;
   const int ct0 = gi * tp.cg;
@@ -847,15 +913,16 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
   // block scan (larger batches); a batch of up to 64 sequences ranks
   // through its first 2 * kWave words
   __shared__ __attribute__((aligned(16))) int2 sm_scan[Lds::scan];
-  static_assert(NTH >= kWave, "rank keys and item counts fit the scan buffer");
+  static_assert(NTH >= kWave && 2 * Lds::scan >= 4 * kWave,
+                "rank keys and item counts (and a second ranking) fit the scan buffer");
   // The plan, in LDS sized by the launch to the batch (mixed_plan_lds), all
   // by position in the order in which sequences deal their items: the
   // sequence and its seq_info (so an item starts its Q and page-id loads
   // without reading the sequence tables again), and the item prefix.
   extern __shared__ __attribute__((aligned(16))) char sm_plan[];
   const int B = p.B;
-  int64_t* const sm_t0 = reinterpret_cast<int64_t*>(sm_plan);
-  int* const sm_slot = reinterpret_cast<int*>(sm_t0 + B);
+  int2* const sm_tp = reinterpret_cast<int2*>(sm_plan);  // (t0, partial base)
+  int* const sm_slot = reinterpret_cast<int*>(sm_tp + B);
   int* const sm_rows = sm_slot + B;
   int* const sm_prior = sm_rows + B;
   int* const sm_order = sm_prior + B;    // the sequence at each position
@@ -869,24 +936,33 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     // sequence, and writes the same tables (identical values from every
     // wave), reading back only what it wrote itself — no barrier.
     const int lane = threadIdx.x & (kWave - 1);
-    int n = 0, key = -1;
-    SeqInfo s{0, 0, 0, 0};
+    int n = 0, key = -1, prows = 0;
+    SeqInfo s{0, 0, 0, 0, 0};  // pbase 0: counted as split
     if (lane < B) {
       s = seq_info(p, lane);
       if (blockIdx.x == 0 && threadIdx.x < kWave && ((s.L + 15) >> 4) > p.n_qtiles)
         set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
       int weight = 0;
-      if (s.L > 0) n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, weight);
+      if (s.L > 0)
+        n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, p.H_q, weight, prows);
       key = n > 0 ? weight : -1;
+      prows = (int)min((int64_t)prows, p.part_cap + 1);
     }
+    // Partial base: the partial rows of the sequences before this one in
+    // sequence order (lanes past B count 0).
+    const int p_incl = wave_inclusive_sum(prows);
+    const int pfx = p_incl - prows;
+    const int ptot = __builtin_amdgcn_readlane(p_incl, kWave - 1);
     // Position: heaviest sequence first, ties by b.  Rank keys (key + 1,
     // clamped to 25 bits, above the lane's complement) are distinct, and a
     // larger one comes earlier; lanes past B write 0, which ranks no one.
     // Every lane reads all keys and item counts by broadcast LDS reads and
     // counts the sequences ahead of it and their items: its position and
     // its item prefix in one pass, with no shuffles.
-    const uint32_t rk =
-        lane < B ? ((uint32_t)min(key + 1, (1 << 25) - 1) << 6) | (uint32_t)(kWave - 1 - lane) : 0u;
+    auto rank_key = [&](int k) {
+      return lane < B ? ((uint32_t)min(k + 1, (1 << 25) - 1) << 6) | (uint32_t)(kWave - 1 - lane) : 0u;
+    };
+    uint32_t rk = rank_key(key);
     uint32_t* const sm_rk = reinterpret_cast<uint32_t*>(sm_scan);  // [kWave]
     int* const sm_rn = reinterpret_cast<int*>(sm_scan) + kWave;     // [kWave]
     sm_rk[lane] = rk;
@@ -900,8 +976,35 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
                 (kk.w > rk ? nn.w : 0);
       tot += nn.x + nn.y + nn.z + nn.w;
     }
+    s.pbase = pfx;
+    if (ptot > p.part_cap) {
+      // The batch's split tiles need more partial rows than the buffer
+      // holds: a sequence whose rows end past it runs unsplit, and the
+      // batch is ranked again with its counts — in arrays of their own, as
+      // another wave may still be reading the first ones.
+      s.pbase = (int64_t)pfx + prows <= p.part_cap ? pfx : -1;
+      if (lane < B && s.pbase < 0 && s.L > 0) {
+        int weight = 0, unused = 0;
+        n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, p.H_q, weight, unused);
+        key = n > 0 ? weight : -1;
+      }
+      rk = rank_key(key);
+      uint32_t* const sm_rk2 = reinterpret_cast<uint32_t*>(sm_scan) + 2 * kWave;  // [kWave]
+      int* const sm_rn2 = reinterpret_cast<int*>(sm_scan) + 3 * kWave;            // [kWave]
+      sm_rk2[lane] = rk;
+      sm_rn2[lane] = n;
+      pos = before = tot = 0;
+      for (int o = 0; o < B; o += 4) {
+        const uint4 kk = *reinterpret_cast<const uint4*>(sm_rk2 + o);
+        const int4 nn = *reinterpret_cast<const int4*>(sm_rn2 + o);
+        pos += (int)(kk.x > rk) + (int)(kk.y > rk) + (int)(kk.z > rk) + (int)(kk.w > rk);
+        before += (kk.x > rk ? nn.x : 0) + (kk.y > rk ? nn.y : 0) + (kk.z > rk ? nn.z : 0) +
+                  (kk.w > rk ? nn.w : 0);
+        tot += nn.x + nn.y + nn.z + nn.w;
+      }
+    }
     if (lane < B) {
-      sm_t0[pos] = s.t0;
+      sm_tp[pos] = int2{(int)s.t0, s.pbase};
       sm_slot[pos] = (int)s.slot;
       sm_rows[pos] = s.L;
       sm_prior[pos] = s.c;
@@ -912,32 +1015,73 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     base = tot;
   } else {
     // Larger batches keep their order (position = sequence): per-sequence
-    // tables and item counts, sequences b = tid, tid + NTH, ...
-    // (B <= kMaxSeqs), then a block scan.
+    // tables, item counts and partial rows, sequences b = tid, tid + NTH,
+    // ... (B <= kMaxSeqs), then a block scan of both: the item prefix and
+    // each sequence's partial base.
     for (int b = threadIdx.x; b < B; b += NTH) {
-      const SeqInfo s = seq_info(p, b);
-      sm_t0[b] = s.t0;
+      const SeqInfo s = seq_info(p, b);  // pbase 0: counted as split
+      sm_tp[b].x = (int)s.t0;
       sm_slot[b] = (int)s.slot;
       sm_rows[b] = s.L;
       sm_prior[b] = s.c;
       if (blockIdx.x == 0 && ((s.L + 15) >> 4) > p.n_qtiles)
         set_err(p.err, CIE_ERRBIT_LEN);  // rows past max_seqlen are not computed
-      int n = 0, weight = 0;
-      if (s.L > 0) n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, weight);
+      int n = 0, weight = 0, prows = 0;
+      if (s.L > 0)
+        n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, p.H_q, weight, prows);
       sm_prefix[b + 1] = n;
+      sm_tp[b].y = (int)min((int64_t)prows, p.part_cap + 1);  // the base, after the scan
       sm_order[b] = b;
     }
     __syncthreads();
-    // item prefix over positions
+    int ptot = 0;
     for (int q0 = 0; q0 < B; q0 += NTH) {
       const int q = q0 + threadIdx.x;
-      const int c = q < B ? sm_prefix[q + 1] : 0;
+      const int2 c = q < B ? int2{sm_prefix[q + 1], sm_tp[q].y} : int2{0, 0};
       const int span = min(NTH, B - q0);
-      const int2 inc = block_scan2<NTH>(int2{c, 0}, sm_scan, span);
-      const int tot = sm_scan[span - 1].x;
-      if (q < B) sm_prefix[q + 1] = base + inc.x;
-      base += tot;
+      const int2 inc = block_scan2<NTH>(c, sm_scan, span);
+      const int2 tot = sm_scan[span - 1];
+      if (q < B) {
+        sm_prefix[q + 1] = base + inc.x;
+        sm_tp[q].y = ptot + inc.y - c.y;  // exclusive
+      }
+      base += tot.x;
+      ptot += tot.y;
       __syncthreads();
+    }
+    if (ptot > p.part_cap) {
+      // The batch's split tiles need more partial rows than the buffer
+      // holds: a sequence whose rows end past it runs unsplit; its item
+      // count is taken again and the item prefix scanned again.
+      for (int b = threadIdx.x; b < B; b += NTH) {
+        SeqInfo s;
+        s.t0 = sm_tp[b].x;
+        s.slot = sm_slot[b];
+        s.L = sm_rows[b];
+        s.c = sm_prior[b];
+        s.pbase = 0;
+        int n = 0, weight = 0, prows = 0;
+        if (s.L > 0)
+          n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, p.H_q, weight, prows);
+        const int pb = sm_tp[b].y;
+        s.pbase = (int64_t)pb + min((int64_t)prows, p.part_cap + 1) <= p.part_cap ? pb : -1;
+        sm_tp[b].y = s.pbase;
+        if (s.pbase < 0 && s.L > 0)
+          n = seq_items<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, p.H_q, weight, prows);
+        sm_prefix[b + 1] = n;
+      }
+      __syncthreads();
+      base = 0;
+      for (int q0 = 0; q0 < B; q0 += NTH) {
+        const int q = q0 + threadIdx.x;
+        const int c = q < B ? sm_prefix[q + 1] : 0;
+        const int span = min(NTH, B - q0);
+        const int2 inc = block_scan2<NTH>(int2{c, 0}, sm_scan, span);
+        const int tot = sm_scan[span - 1].x;
+        if (q < B) sm_prefix[q + 1] = base + inc.x;
+        base += tot;
+        __syncthreads();
+      }
     }
     if (threadIdx.x == 0) sm_prefix[0] = 0;
     __syncthreads();
@@ -961,10 +1105,12 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     const int b = uniform(sm_order[pos]);
     const int j = item - uniform(sm_prefix[pos]);
     SeqInfo s;
-    s.t0 = uniform64(sm_t0[pos]);
+    const int2 tb = sm_tp[pos];
+    s.t0 = uniform(tb.x);
     s.slot = uniform(sm_slot[pos]);
     s.L = uniform(sm_rows[pos]);
     s.c = uniform(sm_prior[pos]);
+    s.pbase = uniform(tb.y);
     int qt, jt;
     seq_locate<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, j, qt, jt);
     MIXED_TRACE(item, 1, __builtin_amdgcn_s_memrealtime());
@@ -1030,14 +1176,14 @@ static int launch_mixed(const MixedParams& p, hipStream_t stream) {
   return (int)hipGetLastError();
 }
 
-// partials: part_m | part_l | part_acc, each region 256-byte aligned
+// partials of `rows` rows: part_m | part_l | part_acc, each region 256-byte
+// aligned
 struct MixedLayout {
   int64_t m, l, acc, total;
 };
 
-static MixedLayout mixed_layout(int64_t total_T, int64_t H_q, int64_t D) {
+static MixedLayout mixed_layout(int64_t rows, int64_t D) {
   auto up = [](int64_t x) { return (x + 255) & ~int64_t(255); };
-  const int64_t rows = total_T * H_q * kMaxChunks;
   MixedLayout w;
   w.m = 0;
   w.l = up(rows * 4);
@@ -1046,13 +1192,24 @@ static MixedLayout mixed_layout(int64_t total_T, int64_t H_q, int64_t D) {
   return w;
 }
 
+// Partial rows a buffer of `bytes` holds (layout total <= bytes).
+static int64_t mixed_partial_rows(int64_t bytes, int64_t D) {
+  const int64_t r = (bytes - 3 * 256) / (4 * (D + 2));
+  return r < 0 ? 0 : (r > kMaxPartRows ? kMaxPartRows : r);
+}
+
+// The default budget: kDefaultRowsPerToken chunk rows per token and q head.
+constexpr int64_t kDefaultRowsPerToken = 2;
+
 }  // namespace cie
 
 using namespace cie;
 
 extern "C" int64_t cie_mixed_partials_bytes(int64_t total_T, int64_t H_q, int64_t D) {
-  if (total_T < 0 || H_q <= 0 || D <= 0) return -1;
-  return mixed_layout(total_T, H_q, D).total;
+  if (total_T < 0 || H_q <= 0 || D <= 0 || total_T > ((int64_t)1 << 40) / H_q) return -1;
+  int64_t rows = kDefaultRowsPerToken * total_T * H_q;
+  if (rows > kMaxPartRows) rows = kMaxPartRows;
+  return mixed_layout(rows, D).total;
 }
 
 extern "C" int64_t cie_mixed_counters(int64_t B, int64_t H_kv, int64_t max_seqlen) {
@@ -1073,26 +1230,30 @@ extern "C" int cie_mixed_trace_buffer(void* buf) {
 extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, const void* v_pool,
                                    const int64_t* cu_seqlens, const int64_t* kv_lens,
                                    const int64_t* slot_ids, const int64_t* block_table,
-                                   void* partials, int32_t* counters, int64_t B, int64_t total_T,
+                                   void* partials, int64_t partials_bytes, int32_t* counters,
+                                   int64_t B, int64_t total_T,
                                    int64_t max_seqlen, int64_t H_q, int64_t H_kv, int64_t D,
                                    int64_t page_size, int64_t n_pages, int64_t pool_page_stride,
                                    int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
                                    int64_t n_slots, int32_t* err, void* stream) {
   if (B < 0 || total_T < 0 || max_seqlen < 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 ||
-      n_pages <= 0 || bt_width <= 0 || bt_stride < bt_width || n_slots <= 0 || page_size <= 0)
+      n_pages <= 0 || bt_width <= 0 || bt_stride < bt_width || n_slots <= 0 || page_size <= 0 ||
+      partials_bytes < 0)
     return CIE_EINVAL;
   if (B == 0 || total_T == 0 || max_seqlen == 0) return CIE_OK;
   if (!o || !q || !k_pool || !v_pool || !cu_seqlens || !kv_lens || !slot_ids || !block_table ||
-      !partials || !counters)
+      (!partials && partials_bytes > 0) || !counters)
     return CIE_EINVAL;
   const int64_t G = H_q / H_kv;
   const int64_t n_qtiles = (max_seqlen + 15) / 16;
-  // item indices (<= total_T tiles x groups x chunks) and a tile's partial
-  // region (16 * H_q rows of kMaxChunks * D floats) must fit in 31 bits
-  if (G > 8 || page_size % 16 != 0 || B > kMaxSeqs || H_kv > 65535 ||
+  // item indices (<= total_T tiles x groups x chunks), a sequence's partial
+  // rows (<= its tokens x H_q x kMaxChunks) and a tile's partial region (16 *
+  // H_q rows of kMaxChunks * D floats) must fit in 31 bits
+  if (G > 8 || page_size % 16 != 0 || B > kMaxSeqs || H_kv > 65535 || H_q > 65535 ||
       n_qtiles > 0x7fffffff || bt_width * page_size > 0x7fffffff ||
       (bt_width * page_size / 16) * (page_size / 16) > 0x7fffffff ||  // magic_div of tile ids
       total_T * kMaxColGroups * kMaxChunks > 0x7fffffff ||
+      total_T * H_q * kMaxChunks > 0x7fffffff ||
       16 * H_q * kMaxChunks * D * 4 > 0x7fffffff)
     return CIE_EUNSUPPORTED;
   if (D != 64 && D != 128) return CIE_EUNSUPPORTED;
@@ -1111,11 +1272,15 @@ extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, c
   p.kv_lens = kv_lens;
   p.slot_ids = slot_ids;
   p.block_table = block_table;
-  const MixedLayout w = mixed_layout(total_T, H_q, D);
+  // The buffer sets the budget of partial rows: sequences whose split tiles
+  // do not fit run unsplit (the plan's pbase).
+  const int64_t cap = mixed_partial_rows(partials_bytes, D);
+  const MixedLayout w = mixed_layout(cap, D);
   char* ws = static_cast<char*>(partials);
   p.part_m = reinterpret_cast<float*>(ws + w.m);
   p.part_l = reinterpret_cast<float*>(ws + w.l);
   p.part_acc = reinterpret_cast<float*>(ws + w.acc);
+  p.part_cap = cap;
   p.counters = counters;
   p.pool_page_stride = pool_page_stride;
   p.pool_head_stride = pool_head_stride;

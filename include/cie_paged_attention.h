@@ -320,8 +320,18 @@ int cie_kv_append_tokens_qkv_rope(void* q_out, void* k_pool, void* v_pool,
  *                not computed (CIE_ERRBIT_LEN).  B <= 1024 (its plan
  *                tables live in LDS: a batch that would take a workgroup
  *                past the device's LDS limit gets CIE_EUNSUPPORTED).
- *   partials   : cie_mixed_partials_bytes(total_T, H_q, D) bytes, 16-byte
- *                aligned, any contents (per-chunk softmax state)
+ *   partials, partials_bytes : a 16-byte aligned buffer of any contents
+ *                (per-chunk softmax state of the tiles the call splits over
+ *                several workgroups); its size is a budget, not a bound the
+ *                call checks against the batch.  Sequences whose split
+ *                tiles' rows (rows x H_q x chunks of each split tile) fit
+ *                the budget, in sequence order, are split; the rest run
+ *                unsplit — same results, longer critical path.  A row takes
+ *                4 * (D + 2) bytes; the budget caps at 2,097,088 rows.
+ *                cie_mixed_partials_bytes(total_T, H_q, D) is the default,
+ *                2 rows per token and q head (about 7.8 MB for 1,052 tokens,
+ *                14 heads, D = 64); partials may be NULL with
+ *                partials_bytes = 0 (nothing splits).
  *   counters   : cie_mixed_counters(B, H_kv, max_seqlen) int32, 16-byte
  *                aligned, zero before the call and left zero by it (an
  *                arrival word and a stale word per query tile and column
@@ -335,7 +345,7 @@ int cie_mixed_attention(void* o, const void* q,
                         const void* k_pool, const void* v_pool,
                         const int64_t* cu_seqlens, const int64_t* kv_lens,
                         const int64_t* slot_ids, const int64_t* block_table,
-                        void* partials, int32_t* counters,
+                        void* partials, int64_t partials_bytes, int32_t* counters,
                         int64_t B, int64_t total_T, int64_t max_seqlen,
                         int64_t H_q, int64_t H_kv, int64_t D,
                         int64_t page_size, int64_t n_pages,

@@ -59,7 +59,12 @@ def test_workspace_sizes(native_lib):
     assert n >= 32 * 14 * 16 * 66 * 4 and n % 256 == 0
     assert native_lib.cie_paged_decode_partials_bytes(-1, 14, 64, 16) == -1
     assert native_lib.cie_paged_decode_max_splits() >= 16
-    assert native_lib.cie_mixed_partials_bytes(1052, 14, 64) >= 1052 * 14 * 16 * 66 * 4
+    # mixed: a budget of 2 chunk rows (D + 2 floats) per token and q head —
+    # 7.8 MB at config 3's 1,052 tokens — capped at 2,097,088 rows
+    n = native_lib.cie_mixed_partials_bytes(1052, 14, 64)
+    assert 2 * 1052 * 14 * 66 * 4 <= n <= 8_000_000 and n % 256 == 0
+    assert native_lib.cie_mixed_partials_bytes(10**6, 64, 128) < 2_097_088 * 130 * 4 + 1024
+    assert native_lib.cie_mixed_partials_bytes(0, 14, 64) >= 0
     assert native_lib.cie_mixed_partials_bytes(10, 0, 64) == -1
     # an arrival word and a stale word per (tile, column group)
     n = native_lib.cie_mixed_counters(32, 2, 256)
@@ -126,10 +131,15 @@ def test_append_and_mixed_reject_bad_arguments(native_lib):
     assert lib.cie_kv_append_decode(8, 8, 8, 8, 64, 64, 64, 64, 8, 8, 8, 1, 2, 16, 64, 10, 2048,
                                     1024, 4, 8, 2, None, None) == -1  # bt_stride < bt_width
     # mixed: G = 14 > 8 is outside the built set
-    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, 32, 1, 4, 4, 14, 1, 64, 16, 10,
+    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, 4096, 32, 1, 4, 4, 14, 1, 64, 16, 10,
                                    1024, 1024, 10, 10, 2, None, None) == -2
     # mixed: counters are required
-    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, None, 1, 4, 4, 14, 2, 64, 16, 10,
+    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, 4096, None, 1, 4, 4, 14, 2, 64, 16, 10,
+                                   1024, 1024, 10, 10, 2, None, None) == -1
+    # mixed: a partials budget without a buffer, and a negative budget
+    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, None, 4096, 32, 1, 4, 4, 14, 2, 64, 16, 10,
+                                   1024, 1024, 10, 10, 2, None, None) == -1
+    assert lib.cie_mixed_attention(16, 16, 16, 16, 8, 8, 8, 8, 16, -1, 32, 1, 4, 4, 14, 2, 64, 16, 10,
                                    1024, 1024, 10, 10, 2, None, None) == -1
 
 

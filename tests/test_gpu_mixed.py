@@ -163,7 +163,7 @@ def test_mixed_pools_near_and_past_4gib(native_lib, n_pages, where):
     err = err_word()
     rc = lib.cie_mixed_attention(o.data_ptr(), c.q.data_ptr(), kp.data_ptr(), vp.data_ptr(),
                                  c.cu_seqlens.data_ptr(), c.kv_lens.data_ptr(), c.slot_ids.data_ptr(),
-                                 bt.data_ptr(), ws.data_ptr(), ctr.data_ptr(), case.B, case.T,
+                                 bt.data_ptr(), ws.data_ptr(), ws.numel(), ctr.data_ptr(), case.B, case.T,
                                  max_seqlen, H_q, 2, D,
                                  16, n_pages, kp.stride(0), kp.stride(1), bt.stride(0),
                                  bt.shape[1], bt.shape[0], err.data_ptr(),
@@ -203,7 +203,7 @@ def test_mixed_partials_above_2gib_in_the_low_address_word(native_lib):
     ctr = torch.zeros(lib.cie_mixed_counters(case.B, 2, 20), dtype=torch.int32, device=DEV)
     rc = lib.cie_mixed_attention(o.data_ptr(), c.q.data_ptr(), kp.data_ptr(), vp.data_ptr(),
                                  c.cu_seqlens.data_ptr(), c.kv_lens.data_ptr(), c.slot_ids.data_ptr(),
-                                 c.block_table.data_ptr(), ptr, ctr.data_ptr(), case.B, case.T,
+                                 c.block_table.data_ptr(), ptr, need, ctr.data_ptr(), case.B, case.T,
                                  20, H_q, 2, D,
                                  16, kp.shape[0], kp.stride(0), kp.stride(1), c.block_table.stride(0),
                                  c.block_table.shape[1], c.block_table.shape[0], None,
@@ -249,7 +249,8 @@ def test_mixed_leaves_rows_outside_sequences_untouched(native_lib):
     ctr = torch.zeros(lib.cie_mixed_counters(case.B, 2, 16), dtype=torch.int32, device=DEV)
     rc = lib.cie_mixed_attention(o.data_ptr(), q.data_ptr(), kp.data_ptr(), vp.data_ptr(),
                                  c.cu_seqlens.data_ptr(), c.kv_lens.data_ptr(), c.slot_ids.data_ptr(),
-                                 c.block_table.data_ptr(), ws.data_ptr(), ctr.data_ptr(), case.B, T_pad,
+                                 c.block_table.data_ptr(), ws.data_ptr(), ws.numel(), ctr.data_ptr(),
+                                 case.B, T_pad,
                                  16, 14, 2, 64,
                                  16, kp.shape[0], kp.stride(0), kp.stride(1), c.block_table.stride(0),
                                  c.block_table.shape[1], c.block_table.shape[0], None,
@@ -336,3 +337,117 @@ def test_mixed_counters_preloaded_negative_are_flagged_then_reset(native_lib):
     assert int(err.item()) == 0
     assert torch.count_nonzero(ctr) == 0
     _check(case, o[0].float().cpu(), "call after the reset")
+
+
+def _split_partial_rows(prior, new, h_q, h_kv, n_qtiles):
+    """Partial rows each sequence's split tiles take, tile by tile: a tile of
+    `rows` rows with k >= 2 chunks holds rows * H_q * k; k = clamp(ceil(pairs
+    / per), 1, 16) for the tile's 32-key steps, per = 4 waves x 8 steps (one
+    column tile) or 4 x 24 (wider)."""
+    G = h_q // h_kv
+    out = []
+    for c, L in zip(prior, new):
+        r = 0
+        for t in range(min((L + 15) // 16, n_qtiles)):
+            rows = min(16, L - 16 * t)
+            n_ctiles = (rows * G + 15) // 16
+            pairs = ((c + 16 * t + rows + 15) // 16 + 1) // 2
+            per = 4 * 8 if n_ctiles == 1 else 4 * 24
+            k = max(1, min(16, -(-pairs // per)))
+            if k > 1:
+                r += rows * h_q * k
+        out.append(r)
+    return out
+
+
+def _budget_bytes(rows, d):
+    """Bytes of a partials buffer that holds exactly `rows` rows (three 256-byte aligned regions)."""
+    return 3 * 256 + rows * 4 * (d + 2)
+
+
+def _mixed_with_budget(case, nbytes, max_seqlen, h_q=14, h_kv=2, d=64):
+    """One mixed call through the C ABI with a partials budget of `nbytes`,
+    inside a buffer with 4 KiB of 0xFF canary past it; returns (o, the
+    buffer's first nbytes, canary intact, counters clean)."""
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    lib = _native.load()
+    buf = torch.full((nbytes + 4096,), 0xFF, dtype=torch.uint8, device=DEV)
+    o = torch.empty_like(c.q)
+    ctr = torch.zeros(lib.cie_mixed_counters(case.B, h_kv, max_seqlen), dtype=torch.int32, device=DEV)
+    err = err_word()
+    rc = lib.cie_mixed_attention(o.data_ptr(), c.q.data_ptr(), kp.data_ptr(), vp.data_ptr(),
+                                 c.cu_seqlens.data_ptr(), c.kv_lens.data_ptr(), c.slot_ids.data_ptr(),
+                                 c.block_table.data_ptr(), buf.data_ptr() if nbytes else None, nbytes,
+                                 ctr.data_ptr(), case.B, case.T, max_seqlen, h_q, h_kv, d,
+                                 16, kp.shape[0], kp.stride(0), kp.stride(1), c.block_table.stride(0),
+                                 c.block_table.shape[1], c.block_table.shape[0], err.data_ptr(),
+                                 _native.stream_handle(torch.device(DEV)))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    canary = bool(torch.all(buf[nbytes:] == 0xFF))
+    return o[0].float().cpu(), buf[:nbytes].cpu(), canary, int(torch.count_nonzero(ctr)) == 0
+
+
+def _written_m_rows(ws, cap):
+    """Rows of part_m (the buffer's first region) a call wrote: 0xFF bytes are NaN, written m never is."""
+    m = ws[:4 * cap].view(torch.float32)
+    return (~torch.isnan(m)).nonzero().flatten()
+
+
+def test_mixed_partials_config3_default_budget(native_lib):
+    """Config 3 takes 784 partial rows (its decode rows split, its prefill
+    chunks do not), well inside the default budget (2 rows per token and
+    head, under 8 MB): the call writes exactly rows [0, 784) of part_m,
+    nothing past its buffer, and matches the oracle."""
+    case = inputs.config3()
+    ms = case.meta["max_seqlen"]
+    need = _split_partial_rows(case.kv_lens.tolist(), case.new_lens.tolist(), 14, 2, (ms + 15) // 16)
+    assert sum(need) == 784
+    nbytes = _native.load().cie_mixed_partials_bytes(case.T, 14, 64)
+    assert nbytes <= 8_000_000
+    note(f"mixed config3 default partials budget ({nbytes} bytes)")
+    o, ws, canary, clean = _mixed_with_budget(case, nbytes, ms)
+    assert canary and clean
+    cap = (nbytes - 768) // (4 * 66)
+    rows = _written_m_rows(ws, cap)
+    assert rows.numel() == 784 and int(rows.max()) == 783
+    _check(case, o, "config3, default partials budget")
+
+
+@pytest.mark.parametrize("B", [24, 90])
+def test_mixed_partials_budget_splits_a_prefix_of_the_batch(native_lib, B):
+    """Sequences take their partial rows in sequence order; one whose rows
+    would end past the budget, and every split sequence after it, runs
+    unsplit.  Budgets of 0, one row short of the need, a part of it and
+    exactly the need give the oracle's output, write exactly the fitting
+    prefix's rows and nothing past the buffer — for the wave plan (B <= 64)
+    and the block plan."""
+    g = torch.Generator().manual_seed(47 + B)
+    prior = torch.randint(0, 3000, (B,), generator=g).tolist()
+    new = [int(x) for x in torch.randint(1, 3, (B,), generator=g)]
+    prior[2], new[2] = 9000, 20      # a prefill tail whose tiles split
+    prior[5], new[5] = 20000, 1      # a decode row of 16 chunks
+    new[7] = 0                       # an empty sequence
+    case = inputs.make_case(prior, new, seed=47 + B)
+    ms = int(max(new))
+    P = _split_partial_rows(prior, new, 14, 2, (ms + 15) // 16)
+    need = sum(P)
+    assert need > 0 and P[2] > 0 and P[5] == 14 * 16
+    want, written = oracle_mixed(case)
+    for cap in (0, need - 1, need // 3, need):
+        nbytes = 0 if cap == 0 else _budget_bytes(cap, 64)
+        note(f"mixed B={B} partials budget {cap} of {need} rows")
+        o, ws, canary, clean = _mixed_with_budget(case, nbytes, ms)
+        assert canary and clean, cap
+        fit, pre = 0, 0
+        for p in P:  # the plan's rule: prefix over all earlier sequences
+            if p and pre + p <= cap:
+                fit += p
+            pre += min(p, cap + 1)
+        if cap:
+            rows = _written_m_rows(ws, cap)
+            assert rows.numel() == fit, (cap, rows.numel(), fit)
+            assert fit == 0 or int(rows.max()) == fit - 1
+        assert_attn_close(o[written], want[written], what=f"budget {cap} of {need}")
