@@ -39,8 +39,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 # HBM bytes per launch of the measured kernel, from rocprofv3 FETCH_SIZE x 2.0 +
 # WRITE_SIZE (scale factors from a plain 256 MiB copy), committed under profiles/
 TRAFFIC_BYTES = {
-    2: (70_976_000, "profiles/hbm_traffic_decode_config2.md"),
-    3: (39_684_279, "profiles/mixed_attention_config3.md"),
+    2: (72_455_782, "profiles/hbm_traffic_decode_config2.md"),
+    3: (39_666_586, "profiles/mixed_attention_config3.md"),
 }
 HBM_PEAK_GBPS = 8000.0
 PLAN_LAYERS = 24  # decode calls per step plan: the layers of config 5's model
