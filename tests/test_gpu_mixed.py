@@ -451,3 +451,22 @@ def test_mixed_partials_budget_splits_a_prefix_of_the_batch(native_lib, B):
             assert rows.numel() == fit, (cap, rows.numel(), fit)
             assert fit == 0 or int(rows.max()) == fit - 1
         assert_attn_close(o[written], want[written], what=f"budget {cap} of {need}")
+
+
+def test_mixed_partials_budget_through_the_python_api(native_lib):
+    """`mixed_gqa_attention(..., partials_bytes=)`: no budget (nothing splits),
+    a tight one and the default give the oracle's output; a negative budget is
+    refused on the host."""
+    case = inputs.make_case([9000, 700, 3000, 20000], [20, 1, 2, 1], seed=71)
+    c = case.to(DEV)
+    kp, vp = (t.to(DEV) for t in case.appended_pools())
+    want, written = oracle_mixed(case)
+    for nbytes in (0, _budget_bytes(14 * 16, 64), None):
+        note(f"mixed python api partials_bytes={nbytes}")
+        o = mixed_gqa_attention(c.q, kp, vp, 20, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
+                                partials_bytes=nbytes)
+        torch.cuda.synchronize()
+        assert_attn_close(o[0].float().cpu()[written], want[written], what=f"partials_bytes={nbytes}")
+    with pytest.raises(AssertionError):
+        mixed_gqa_attention(c.q, kp, vp, 20, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
+                            partials_bytes=-1)
