@@ -806,6 +806,12 @@ def bench_mixed(args, cie, inputs, ref, dev):
     us_mix, _ = time_calls([mixed_only(i) for i in range(R)], args.steps, args.warmup, not args.no_graph,
                            args.repeats)
     log(f"config 3: {us:.2f} us/call (append + mixed), mixed kernel alone {us_mix:.2f} us/launch")
+    # Planned launches: a mixed step makes one plan (mixed_plan) for all of
+    # its layers, so the timed sequence launches the plan once per
+    # PLAN_LAYERS calls, inside the timed region.
+    us_mix_planned, err_planned = time_mixed_planned(cie, layers, c, case, 256, 14, args)
+    log(f"planned: mixed kernel {us_mix_planned:.2f} us/launch (1 plan per {PLAN_LAYERS} launches), "
+        f"planned == unplanned: {err_planned}")
     E = (case.kv_lens + case.new_lens).tolist()
     kv_bytes = 2 * sum(E) * 2 * 64 * 2
     qo = 2 * case.T * 14 * 64 * 2
@@ -823,6 +829,7 @@ def bench_mixed(args, cie, inputs, ref, dev):
         "achieved_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
         "achieved_TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
         "us_mixed_kernel": round(us_mix, 3),
+        "us_mixed_kernel_planned": round(us_mix_planned, 3),
         "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
         "config": {"workload": {"all": "config 3 mixed: 4x256-row prefill chunks + 28 decode rows",
                                 "prefill": "config 3's 4x256-row prefill chunks alone",
@@ -836,6 +843,40 @@ def bench_mixed(args, cie, inputs, ref, dev):
                      "traffic_source": TRAFFIC_BYTES[3][1] if args.mixed_part == "all" else None},
         "parity_max_abs_err": err,
     }), flush=True)
+
+
+def time_mixed_planned(cie, layers, c, case, max_seqlen: int, h_q: int, args):
+    """us per planned mixed launch over the rotating layers, the plan made once
+    per PLAN_LAYERS launches inside the timed region; and whether layer 0's
+    planned output equals its unplanned one bit for bit."""
+    R = len(layers)
+    holder = [None]
+
+    def make_plan():
+        holder[0] = cie.mixed_plan(layers[0].kp, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
+                                   max_seqlen, case.T, h_q)
+
+    def planned(k):
+        L = layers[k % R]
+
+        def f():
+            if k == 0:
+                make_plan()
+            cie.mixed_gqa_attention(L.q, L.kp, L.vp, max_seqlen, c.cu_seqlens, c.kv_lens, c.slot_ids,
+                                    c.block_table, plan=holder[0])
+        return f
+    make_plan()
+    L = layers[0]
+    o_u = cie.mixed_gqa_attention(L.q, L.kp, L.vp, max_seqlen, c.cu_seqlens, c.kv_lens, c.slot_ids,
+                                  c.block_table)
+    o_p = cie.mixed_gqa_attention(L.q, L.kp, L.vp, max_seqlen, c.cu_seqlens, c.kv_lens, c.slot_ids,
+                                  c.block_table, plan=holder[0])
+    torch.cuda.synchronize()
+    rows = int(case.cu_seqlens[-1])
+    same = bool(torch.equal(o_u[0, :rows], o_p[0, :rows]))
+    us, _ = time_calls([planned(k) for k in range(PLAN_LAYERS)], args.steps, args.warmup, not args.no_graph,
+                       args.repeats)
+    return us, same
 
 
 # mixed_gqa_attention_kernel us/call at T = 128 by batch size, RTX 4070 Laptop
@@ -874,10 +915,13 @@ def bench_feature_shapes(args, cie, inputs, ref, dev, tokens: int = 128, context
             return lambda: cie.mixed_gqa_attention(L.q, L.kp, L.vp, tokens, c.cu_seqlens, c.kv_lens, c.slot_ids,
                                                    c.block_table)
         us, _ = time_calls([call(i) for i in range(R)], args.steps, args.warmup, not args.no_graph, args.repeats)
+        us_p, same = time_mixed_planned(cie, layers, c, case, tokens, 14, args)
         pub = PUBLISHED_MIXED_T128[B]
-        log(f"feature-bench shape B={B}: {us:.2f} us (reference, RTX 4070 Laptop: {pub} us), err {err:.1e}")
-        table.append({"batch": B, "us_per_call": round(us, 2), "published_us": pub,
-                      "speedup_vs_published": round(pub / us, 2), "parity_max_abs_err": err})
+        log(f"feature-bench shape B={B}: {us:.2f} us, planned {us_p:.2f} us (reference, RTX 4070 Laptop: "
+            f"{pub} us), err {err:.1e}, planned == unplanned: {same}")
+        table.append({"batch": B, "us_per_call": round(us, 2), "us_per_call_planned": round(us_p, 2),
+                      "published_us": pub, "speedup_vs_published": round(pub / us, 2),
+                      "parity_max_abs_err": err, "planned_equals_unplanned": same})
     b32 = table[-1]
     print(json.dumps({
         "metric": "mixed attention us/call at the reference feature-bench shape (T=128, context 256)",

@@ -21,8 +21,10 @@ from .attn.core import (  # noqa: F401
     gqa_decode_plan_op,
     gqa_decode_qkv_rope_attention_op,
     gqa_mixed_attention_op,
+    gqa_mixed_plan_op,
     kv_append_tokens_qkv_rope_op,
     mixed_gqa_attention,
+    mixed_plan,
     replace_attention,
     reset_split_counters,
     use_triton_attention,

@@ -97,6 +97,18 @@ _SIGNATURES = {
          _c_i64, _c_ptr, _c_ptr],
     ),
     "cie_mixed_partials_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "cie_mixed_plan_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "cie_mixed_plan": (
+        ctypes.c_int,
+        [_c_ptr, _c_i64, _c_i64p, _c_i64p, _c_i64p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
+    "cie_mixed_attention_planned": (
+        ctypes.c_int,
+        [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64p, _c_ptr, _c_i64, _c_ptr,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_i64, _c_ptr, _c_ptr],
+    ),
     "cie_mixed_counters": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "cie_mixed_attention": (
         ctypes.c_int,
@@ -106,7 +118,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -434,9 +434,47 @@ def _as_rows(x: torch.Tensor, h_kv: int, d: int) -> torch.Tensor:
     return rows
 
 
+def mixed_plan(k_cache, cu_seqlens, kv_lens, slot_ids, block_table, max_seqlen: int, total_T: int,
+               num_heads: int, partials_bytes=None, err=None):
+    """One mixed step's plan, made once and used by every layer's planned mixed attention.
+
+    A mixed step's sequences (``cu_seqlens``, ``kv_lens`` = prior lengths,
+    ``slot_ids``) are the same for every layer (the reference builds its
+    ``AttentionMetadata`` once per step, attn/metadata.py:3-55): the plan holds
+    the work items, their order and the partial bases that each launch of
+    ``mixed_gqa_attention`` would otherwise work out for itself.  Pass it as
+    ``plan=`` to the layers' calls with the same batch, ``total_T`` (q's
+    packed rows), head count and ``partials_bytes``; the outputs are the
+    unplanned ones bit for bit.  Returns an int32 device tensor.
+    """
+    N_PAGES, H_kv, PAGE_SIZE, D = k_cache.shape
+    B = slot_ids.shape[0]
+    _require(num_heads % H_kv == 0, "H_q must be a multiple of H_kv")
+    _require(tuple(cu_seqlens.shape) == (B + 1,) and tuple(kv_lens.shape) == (B,),
+             "cu_seqlens must be (B+1,) and kv_lens (B,)")
+    _require(N_PAGES == block_table.shape[1], "block_table width must equal n_pages")
+    dev = _native.require_device(k_cache, cu_seqlens, kv_lens, slot_ids, block_table)
+    cu_seqlens, kv_lens, slot_ids = _index(cu_seqlens), _index(kv_lens), _index(slot_ids)
+    lib = _native.load()
+    n = lib.cie_mixed_plan_bytes(B, int(total_T))
+    _require(n > 0, "batch too large for a mixed plan")
+    plan = torch.empty(n // 4, dtype=torch.int32, device=dev)
+    if partials_bytes is None:
+        partials_bytes = lib.cie_mixed_partials_bytes(int(total_T), num_heads, D)
+    _native.check(
+        lib.cie_mixed_plan(
+            plan.data_ptr(), n, cu_seqlens.data_ptr(), kv_lens.data_ptr(), slot_ids.data_ptr(), B,
+            int(total_T), int(max_seqlen), num_heads, H_kv, D, PAGE_SIZE, block_table.shape[1],
+            block_table.shape[0], partials_bytes, _native.ptr(err), _native.stream_handle(dev),
+        ),
+        "cie_mixed_plan",
+    )
+    return plan
+
+
 def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids, block_table,
                         BLOCK_M=16, BLOCK_N=64, num_warps=4, wrap=None, err=None, counters=None,
-                        partials_bytes=None):
+                        partials_bytes=None, plan=None):
     """Varlen causal GQA attention over the paged pool (chunked prefill + decode).
 
     q: (1, total_T, H_q, D) fp16 contiguous; cu_seqlens (B+1,); kv_lens (B,) =
@@ -445,6 +483,8 @@ def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids,
     ``partials_bytes`` is the budget of split-chunk partial state (default
     ``cie_mixed_partials_bytes``: 2 rows per token and q head); sequences
     whose split tiles do not fit it run unsplit, with the same results.
+    ``plan``: the step's ``mixed_plan`` (same batch, ``total_T``, heads and
+    budget); ``cu_seqlens``, ``kv_lens`` and ``slot_ids`` are then read from it.
     """
     total_T, H_q, D = q.shape[1:]
     N_PAGES, H_kv, PAGE_SIZE, _ = k.shape
@@ -471,6 +511,22 @@ def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids,
     if counters is None:
         counters = split_counters(dev, n_ctr)
     _require(counters.dtype == torch.int32 and counters.numel() >= n_ctr, "counters too small")
+    if plan is not None:  # a step's plan (mixed_plan)
+        n = lib.cie_mixed_plan_bytes(B, total_T)
+        _require(plan.dtype == torch.int32 and plan.is_contiguous() and plan.numel() * 4 >= n,
+                 "plan must come from mixed_plan for this batch")
+        _native.check(
+            lib.cie_mixed_attention_planned(
+                o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), plan.data_ptr(), plan.numel() * 4,
+                block_table.data_ptr(),
+                _native.ptr(partials) if partials_bytes else None, partials_bytes, counters.data_ptr(),
+                B, total_T, int(max_seqlen), H_q, H_kv, D, PAGE_SIZE, N_PAGES,
+                k.stride(0), k.stride(1), block_table.stride(0), block_table.shape[1],
+                block_table.shape[0], _native.ptr(err), _native.stream_handle(dev),
+            ),
+            "cie_mixed_attention_planned",
+        )
+        return o
     _native.check(
         lib.cie_mixed_attention(
             o.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
@@ -572,16 +628,30 @@ def _(qkv, cos, sin, k_cache, v_cache, pages, offsets, num_heads):
 def gqa_mixed_attention_op(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     max_seqlen: int, cu_seqlens: torch.Tensor, kv_lens: torch.Tensor,
-    slot_ids: torch.Tensor, block_table: torch.Tensor,
+    slot_ids: torch.Tensor, block_table: torch.Tensor, plan: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     return mixed_gqa_attention(q, k, v, **GQA_PREFILL_CONFIG, max_seqlen=max_seqlen,
                                cu_seqlens=cu_seqlens, block_table=block_table, kv_lens=kv_lens,
-                               slot_ids=slot_ids)
+                               slot_ids=slot_ids, plan=plan)
 
 
 @gqa_mixed_attention_op.register_fake
-def _(q, k, v, max_seqlen, cu_seqlens, kv_lens, slot_ids, block_table):
+def _(q, k, v, max_seqlen, cu_seqlens, kv_lens, slot_ids, block_table, plan=None):
     return torch.empty_like(q)
+
+
+@torch.library.custom_op("inference::gqa_mixed_plan", mutates_args=())
+def gqa_mixed_plan_op(k_cache: torch.Tensor, cu_seqlens: torch.Tensor, kv_lens: torch.Tensor,
+                      slot_ids: torch.Tensor, block_table: torch.Tensor, max_seqlen: int, total_T: int,
+                      num_heads: int) -> torch.Tensor:
+    """A mixed step's plan for its layers' mixed attention (mixed_plan)."""
+    return mixed_plan(k_cache, cu_seqlens, kv_lens, slot_ids, block_table, max_seqlen, total_T, num_heads)
+
+
+@gqa_mixed_plan_op.register_fake
+def _(k_cache, cu_seqlens, kv_lens, slot_ids, block_table, max_seqlen, total_T, num_heads):
+    n = _native.load().cie_mixed_plan_bytes(slot_ids.shape[0], total_T)
+    return k_cache.new_empty((n // 4,), dtype=torch.int32)
 
 
 class TritonQwen2Attention(torch.nn.Module):
@@ -641,7 +711,7 @@ class TritonQwen2Attention(torch.nn.Module):
             if metadata.full_decode:
                 o = gqa_decode_qkv_rope_attention_op(
                     qkv, cos, sin, keys, values, kv_manager.lens, metadata.slot_ids,
-                    kv_manager.block_table, self.num_heads, plan=metadata.decode_plan,
+                    kv_manager.block_table, self.num_heads, plan=getattr(metadata, "decode_plan", None),
                 )
             else:
                 query_states = kv_append_tokens_qkv_rope_op(
@@ -651,7 +721,7 @@ class TritonQwen2Attention(torch.nn.Module):
                     query_states, keys, values,
                     kv_lens=kv_manager.lens[metadata.slot_ids], max_seqlen=metadata.max_seqlen,
                     cu_seqlens=metadata.cu_seqlens, slot_ids=metadata.slot_ids,
-                    block_table=kv_manager.block_table,
+                    block_table=kv_manager.block_table, plan=getattr(metadata, "mixed_plan", None),
                 )
             attn_output = attn.o_proj(o.reshape(1, total_T, self.num_heads * self.head_dim))
             return attn_output, None
@@ -672,7 +742,7 @@ class TritonQwen2Attention(torch.nn.Module):
             o = gqa_decode_append_attention_op(
                 query_states, kv_manager.keys[self.layer_idx], kv_manager.values[self.layer_idx],
                 key_states, value_states, kv_manager.lens, metadata.slot_ids, kv_manager.block_table,
-                plan=metadata.decode_plan,
+                plan=getattr(metadata, "decode_plan", None),
             )
         elif metadata.full_decode:
             kv_manager.decode_update(self.layer_idx, metadata.slot_ids, key_states, value_states)
@@ -688,7 +758,7 @@ class TritonQwen2Attention(torch.nn.Module):
                 query_states, kv_manager.keys[self.layer_idx], kv_manager.values[self.layer_idx],
                 kv_lens=kv_manager.lens[metadata.slot_ids], max_seqlen=metadata.max_seqlen,
                 cu_seqlens=metadata.cu_seqlens, slot_ids=metadata.slot_ids,
-                block_table=kv_manager.block_table,
+                block_table=kv_manager.block_table, plan=getattr(metadata, "mixed_plan", None),
             )
         attn_output = attn.o_proj(o.reshape(1, total_T, self.num_heads * self.head_dim))
         return attn_output, None

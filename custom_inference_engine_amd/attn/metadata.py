@@ -24,6 +24,8 @@ class AttentionMetadata:
         # a decode step's plan (inference::gqa_decode_plan), made once per
         # step by the step module and read by every layer; None: unplanned
         self.decode_plan = None
+        # a mixed step's plan (inference::gqa_mixed_plan), likewise
+        self.mixed_plan = None
 
     def prepare_full_graph(self, batch_size: int) -> None:
         self.slot_ids = torch.zeros((batch_size,), dtype=torch.long, device=self.device)

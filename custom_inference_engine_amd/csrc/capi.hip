@@ -1,7 +1,7 @@
 // Library-level entry points of the C ABI (version, status strings).
 #include "cie_common.h"
 
-extern "C" int cie_abi_version(void) { return 9; }
+extern "C" int cie_abi_version(void) { return 10; }
 
 extern "C" const char* cie_status_string(int status) {
   switch (status) {

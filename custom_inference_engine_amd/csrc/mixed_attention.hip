@@ -159,6 +159,11 @@ struct MixedParams {
   uint32_t pool_bytes;          // bytes of each pool if under 4 GiB, else 0
   float scale_log2;
   int32_t* err;
+  // planned launches: the step's plan (cie_mixed_plan) and its capacity in
+  // items; the plan kernel writes `plan_out`
+  const int32_t* plan;
+  int32_t* plan_out;
+  int32_t plan_cap;
 };
 
 struct SeqInfo {
@@ -600,6 +605,11 @@ __device__ __forceinline__ void merge_group(const MixedParams& p, const SeqInfo&
 }
 
 constexpr int kMaxSeqs = 1024;  // sequences a launch can plan (LDS plan tables)
+// A step's plan (cie_mixed_plan): kPlanHeader header words, then 8 words per
+// item; a planned launch stages the descriptors of its first kDescRounds
+// rounds in LDS.
+constexpr int kPlanHeader = 8;
+constexpr int kDescRounds = 16;
 constexpr int kRankSeqs = 64;   // batches up to this size deal their items heaviest first
 static_assert(kRankSeqs == kWave, "a batch small enough to rank is planned by one wave");
 
@@ -896,40 +906,53 @@ constexpr bool mixed_lds_fits() {
   return MixedLds<D>::bytes + mixed_plan_lds(kMaxSeqs) <= kLdsPerWorkgroup;
 }
 
-template <int D, bool P32>
-__global__ __launch_bounds__(mixed_waves<D>() * kWave)
-__attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_attention_kernel(
-    MixedParams p) {
-  static_assert(col_group<D>() <= 4 && 8 / col_group<D>() <= kMaxColGroups, "column groups");
-  static_assert(mixed_lds_fits<D>(),
-                "static LDS + the plan tables of kMaxSeqs sequences exceed a workgroup's LDS");
+// The batch's plan tables in LDS (sm_plan, mixed_plan_lds(B) bytes), all by
+// position in the order in which sequences deal their items: the sequence
+// and its seq_info (so an item starts its Q and page-id loads without
+// reading the sequence tables again), and the item prefix.
+struct PlanTables {
+  int2* tp;     // (t0, partial base)
+  int* slot;
+  int* rows;
+  int* prior;
+  int* order;   // the sequence at each position
+  int* prefix;  // B + 1 entries, by position
+  __device__ __forceinline__ PlanTables(char* sm, int B) {
+    tp = reinterpret_cast<int2*>(sm);
+    slot = reinterpret_cast<int*>(tp + B);
+    rows = slot + B;
+    prior = rows + B;
+    order = prior + B;
+    prefix = order + B;
+  }
+  __device__ __forceinline__ SeqInfo seq(int pos) const {
+    SeqInfo s;
+    const int2 tb = tp[pos];
+    s.t0 = uniform(tb.x);
+    s.slot = uniform(slot[pos]);
+    s.L = uniform(rows[pos]);
+    s.c = uniform(prior[pos]);
+    s.pbase = uniform(tb.y);
+    return s;
+  }
+};
+
+// Plans the batch into the tables (every workgroup of an unplanned launch
+// does this; a planned launch reads the result from cie_mixed_plan):
+// per-sequence item counts, partial bases and the dealing order; returns
+// the item count (uniform).
+template <int D>
+__device__ __forceinline__ int plan_batch(const MixedParams& p, const PlanTables& t, int2* sm_scan) {
   constexpr int W = mixed_waves<D>();
   constexpr int NTH = W * kWave;
-  typedef MixedLds<D> Lds;
-  __shared__ f32x4 sm_facc[Lds::facc];
-  __shared__ float2 sm_fml[Lds::fml];
-  __shared__ f16x8 sm_q[Lds::q];
-  __shared__ int sm_last;
-  // block scan (larger batches); a batch of up to 64 sequences ranks
-  // through its first 2 * kWave words
-  __shared__ __attribute__((aligned(16))) int2 sm_scan[Lds::scan];
-  static_assert(NTH >= kWave && 2 * Lds::scan >= 4 * kWave,
-                "rank keys and item counts (and a second ranking) fit the scan buffer");
-  // The plan, in LDS sized by the launch to the batch (mixed_plan_lds), all
-  // by position in the order in which sequences deal their items: the
-  // sequence and its seq_info (so an item starts its Q and page-id loads
-  // without reading the sequence tables again), and the item prefix.
-  extern __shared__ __attribute__((aligned(16))) char sm_plan[];
-  const int B = p.B;
-  int2* const sm_tp = reinterpret_cast<int2*>(sm_plan);  // (t0, partial base)
-  int* const sm_slot = reinterpret_cast<int*>(sm_tp + B);
-  int* const sm_rows = sm_slot + B;
-  int* const sm_prior = sm_rows + B;
-  int* const sm_order = sm_prior + B;    // the sequence at each position
-  int* const sm_prefix = sm_order + B;   // B + 1 entries, by position
-
   constexpr int CG = col_group<D>();
-  MIXED_TRACE(0, 15, __builtin_amdgcn_s_memrealtime());  // workgroup start
+  const int B = p.B;
+  int2* const sm_tp = t.tp;
+  int* const sm_slot = t.slot;
+  int* const sm_rows = t.rows;
+  int* const sm_prior = t.prior;
+  int* const sm_order = t.order;
+  int* const sm_prefix = t.prefix;
   int base = 0;
   if (B <= kWave) {
     // A batch of up to 64 sequences: every wave plans it alone, a lane per
@@ -1086,10 +1109,68 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
     if (threadIdx.x == 0) sm_prefix[0] = 0;
     __syncthreads();
   }
-  const int n_items = uniform(base);
+  return uniform(base);
+}
+
+template <int D, bool P32, bool kPlanned>
+__global__ __launch_bounds__(mixed_waves<D>() * kWave)
+__attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_attention_kernel(
+    MixedParams p) {
+  static_assert(col_group<D>() <= 4 && 8 / col_group<D>() <= kMaxColGroups, "column groups");
+  static_assert(mixed_lds_fits<D>(),
+                "static LDS + the plan tables of kMaxSeqs sequences exceed a workgroup's LDS");
+  constexpr int W = mixed_waves<D>();
+  constexpr int NTH = W * kWave;
+  typedef MixedLds<D> Lds;
+  __shared__ f32x4 sm_facc[Lds::facc];
+  __shared__ float2 sm_fml[Lds::fml];
+  __shared__ f16x8 sm_q[Lds::q];
+  __shared__ int sm_last;
+  // block scan (larger batches); a batch of up to 64 sequences ranks
+  // through its first 2 * kWave words
+  __shared__ __attribute__((aligned(16))) int2 sm_scan[Lds::scan];
+  static_assert(NTH >= kWave && 2 * Lds::scan >= 4 * kWave,
+                "rank keys and item counts (and a second ranking) fit the scan buffer");
+  // Unplanned launches: the plan tables, in LDS sized by the launch to the
+  // batch (mixed_plan_lds).  Planned launches: the descriptors of this
+  // workgroup's first kDescRounds items.
+  extern __shared__ __attribute__((aligned(16))) char sm_plan[];
+  __shared__ __attribute__((aligned(16))) int4 sm_desc[kPlanned ? 2 * kDescRounds : 1];
+  const PlanTables tables(sm_plan, p.B);
+
+  constexpr int CG = col_group<D>();
+  MIXED_TRACE(0, 15, __builtin_amdgcn_s_memrealtime());  // workgroup start
   const int g = blockIdx.x % p.H_kv;
   const int slot_r = blockIdx.x / p.H_kv;
   const int n_slots_r = gridDim.x / p.H_kv;  // workgroups per kv head
+  // item of round q for this workgroup (see the item loop)
+  auto item_of = [&](int q) { return q * n_slots_r + ((q & 1) ? n_slots_r - 1 - slot_r : slot_r); };
+  int n_items;
+  if constexpr (kPlanned) {
+    // The step's plan: a header, then one 8-word descriptor per item.  The
+    // header and the descriptors of this workgroup's first kDescRounds
+    // rounds are loaded together (one memory round trip; a descriptor past
+    // the item count is never used), the descriptors into LDS.
+    const int32_t* const hdr = p.plan;
+    const int tid = threadIdx.x;
+    if (tid < 2 * kDescRounds) {
+      const int it = item_of(tid >> 1);
+      if (it < p.plan_cap)
+        sm_desc[tid] = *reinterpret_cast<const int4*>(p.plan + kPlanHeader + (int64_t)it * 8 + 4 * (tid & 1));
+    }
+    const int4 h0 = *reinterpret_cast<const int4*>(hdr);
+    const int4 h1 = *reinterpret_cast<const int4*>(hdr + 4);
+    __syncthreads();
+    n_items = uniform(h0.x);
+    // a plan made for another batch shape, budget or partial layout
+    if (uniform(h0.y) != (int)p.part_cap || uniform(h0.z) != p.B || uniform(h0.w) != p.n_qtiles ||
+        uniform(h1.x) != p.H_q || uniform(h1.y) != p.H_kv || n_items > p.plan_cap) {
+      if (blockIdx.x == 0 && threadIdx.x == 0) set_err(p.err, CIE_ERRBIT_PLAN);
+      return;
+    }
+  } else {
+    n_items = plan_batch<D>(p, tables, sm_scan);
+  }
   MIXED_TRACE(0, 6, __builtin_amdgcn_s_memrealtime());  // planning done
   MIXED_TRACE(0, 14, (uint64_t)blockIdx.x);
 
@@ -1098,25 +1179,89 @@ __attribute__((amdgpu_waves_per_eu(mixed_waves_per_simd<D>()))) void mixed_atten
   // workgroups that took the heaviest items of round 0 take the lightest of
   // round 1.
   for (int q = 0; slot_r < n_slots_r; ++q) {
-    const int item = q * n_slots_r + ((q & 1) ? n_slots_r - 1 - slot_r : slot_r);
+    const int item = item_of(q);
     if (item >= n_items) break;
     MIXED_TRACE(item, 0, __builtin_amdgcn_s_memrealtime());
-    const int pos = prefix_search(sm_prefix, B, item);
-    const int b = uniform(sm_order[pos]);
-    const int j = item - uniform(sm_prefix[pos]);
+    int b, qt, jt;
     SeqInfo s;
-    const int2 tb = sm_tp[pos];
-    s.t0 = uniform(tb.x);
-    s.slot = uniform(sm_slot[pos]);
-    s.L = uniform(sm_rows[pos]);
-    s.c = uniform(sm_prior[pos]);
-    s.pbase = uniform(tb.y);
-    int qt, jt;
-    seq_locate<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, j, qt, jt);
+    if constexpr (kPlanned) {
+      int4 d0, d1;
+      if (q < kDescRounds) {
+        d0 = sm_desc[2 * q];
+        d1 = sm_desc[2 * q + 1];
+      } else {
+        d0 = *reinterpret_cast<const int4*>(p.plan + kPlanHeader + (int64_t)item * 8);
+        d1 = *reinterpret_cast<const int4*>(p.plan + kPlanHeader + (int64_t)item * 8 + 4);
+      }
+      b = uniform(d0.x);
+      qt = uniform(d0.y);
+      jt = uniform(d0.z);
+      s.t0 = uniform(d0.w);
+      s.slot = uniform(d1.x);
+      s.L = uniform(d1.y);
+      s.c = uniform(d1.z);
+      s.pbase = uniform(d1.w);
+    } else {
+      const int pos = prefix_search(tables.prefix, p.B, item);
+      b = uniform(tables.order[pos]);
+      const int j = item - uniform(tables.prefix[pos]);
+      s = tables.seq(pos);
+      seq_locate<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, j, qt, jt);
+    }
     MIXED_TRACE(item, 1, __builtin_amdgcn_s_memrealtime());
     MIXED_TRACE(item, 7, (uint64_t)(b * 1000 + qt));
     process_item<D, P32>(p, s, b, g, uniform(qt), uniform(jt), sm_facc, sm_fml, sm_q, &sm_last,
                          item);
+  }
+}
+
+
+// A step's plan for its planned mixed launches (cie_mixed_plan): one
+// workgroup plans the batch as every workgroup of an unplanned launch does,
+// then writes the header {items, partial budget (rows), B, query tiles,
+// H_q, H_kv, 0, 0} and, per item in dealing order, its descriptor
+// {b, query tile, index in tile, t0, slot, rows, prior, partial base}.
+template <int D>
+__global__ __launch_bounds__(mixed_waves<D>() * kWave) void mixed_plan_kernel(MixedParams p) {
+  constexpr int W = mixed_waves<D>();
+  constexpr int NTH = W * kWave;
+  constexpr int CG = col_group<D>();
+  typedef MixedLds<D> Lds;
+  __shared__ __attribute__((aligned(16))) int2 sm_scan[Lds::scan];
+  extern __shared__ __attribute__((aligned(16))) char sm_plan[];
+  const PlanTables t(sm_plan, p.B);
+  const int n_items = plan_batch<D>(p, t, sm_scan);
+  __syncthreads();
+  int32_t* const out = p.plan_out;
+  const bool fits = n_items <= p.plan_cap;
+  if (threadIdx.x == 0) {
+    // a batch with more items than the capacity (only overlapping
+    // sequences can exceed it) gets an empty plan and CIE_ERRBIT_PLAN
+    if (!fits) set_err(p.err, CIE_ERRBIT_PLAN);
+    *reinterpret_cast<int4*>(out) = int4{fits ? n_items : 0, (int)p.part_cap, p.B, p.n_qtiles};
+    *reinterpret_cast<int4*>(out + 4) = int4{p.H_q, p.H_kv, 0, 0};
+  }
+  if (!fits) return;
+  for (int i = threadIdx.x; i < n_items; i += NTH) {
+    // the last position whose prefix is at or below i (prefix[0] = 0)
+    int lo = 0, hi = p.B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (t.prefix[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    const int2 tb = t.tp[lo];
+    SeqInfo s;
+    s.t0 = tb.x;
+    s.slot = t.slot[lo];
+    s.L = t.rows[lo];
+    s.c = t.prior[lo];
+    s.pbase = tb.y;
+    int qt, jt;
+    seq_locate<CG, W>(s, seq_tiles<CG, W>(s, p.n_qtiles, p.G), p.G, i - t.prefix[lo], qt, jt);
+    int32_t* const d = out + kPlanHeader + (int64_t)i * 8;
+    *reinterpret_cast<int4*>(d) = int4{t.order[lo], qt, jt, (int)s.t0};
+    *reinterpret_cast<int4*>(d + 4) = int4{(int)s.slot, s.L, s.c, s.pbase};
   }
 }
 
@@ -1146,33 +1291,48 @@ static int64_t device_lds_limit() {
   return lim[dev];
 }
 
-template <int D, bool P32>
+template <class K>
+static int64_t static_lds_of(K kernel) {
+  hipFuncAttributes a{};
+  return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(kernel)) == hipSuccess
+             ? (int64_t)a.sharedSizeBytes
+             : 0;
+}
+
+template <int D, bool P32, bool kPlanned>
 static int64_t mixed_static_lds() {
   static int64_t bytes = -1;
-  if (bytes < 0) {
-    hipFuncAttributes a{};
-    bytes = hipFuncGetAttributes(&a, reinterpret_cast<const void*>(mixed_attention_kernel<D, P32>)) ==
-                    hipSuccess
-                ? (int64_t)a.sharedSizeBytes
-                : 0;
-  }
+  if (bytes < 0) bytes = static_lds_of(mixed_attention_kernel<D, P32, kPlanned>);
   return bytes;
 }
 
-template <int D>
+template <int D, bool kPlanned>
 static int launch_mixed(const MixedParams& p, hipStream_t stream) {
   dim3 grid(mixed_workgroups(p.H_kv), 1, 1);
   // a batch whose plan tables would take the workgroup past the device's
-  // LDS is refused here (the dispatch itself would be rejected)
-  const int64_t lds = (p.pool_bytes != 0 ? mixed_static_lds<D, true>() : mixed_static_lds<D, false>()) +
-                      (int64_t)mixed_plan_lds(p.B);
+  // LDS is refused here (the dispatch itself would be rejected); a planned
+  // launch reads its plan instead of building the tables
+  const size_t dyn = kPlanned ? 0 : mixed_plan_lds(p.B);
+  const int64_t lds = (p.pool_bytes != 0 ? mixed_static_lds<D, true, kPlanned>()
+                                         : mixed_static_lds<D, false, kPlanned>()) +
+                      (int64_t)dyn;
   if (lds > device_lds_limit()) return CIE_EUNSUPPORTED;
   if (p.pool_bytes != 0)
-    hipLaunchKernelGGL((mixed_attention_kernel<D, true>), grid, dim3(mixed_waves<D>() * kWave),
-                       mixed_plan_lds(p.B), stream, p);
+    hipLaunchKernelGGL((mixed_attention_kernel<D, true, kPlanned>), grid,
+                       dim3(mixed_waves<D>() * kWave), dyn, stream, p);
   else
-    hipLaunchKernelGGL((mixed_attention_kernel<D, false>), grid, dim3(mixed_waves<D>() * kWave),
-                       mixed_plan_lds(p.B), stream, p);
+    hipLaunchKernelGGL((mixed_attention_kernel<D, false, kPlanned>), grid,
+                       dim3(mixed_waves<D>() * kWave), dyn, stream, p);
+  return (int)hipGetLastError();
+}
+
+template <int D>
+static int launch_mixed_plan(const MixedParams& p, hipStream_t stream) {
+  static int64_t st = -1;
+  if (st < 0) st = static_lds_of(mixed_plan_kernel<D>);
+  if (st + (int64_t)mixed_plan_lds(p.B) > device_lds_limit()) return CIE_EUNSUPPORTED;
+  hipLaunchKernelGGL((mixed_plan_kernel<D>), dim3(1), dim3(mixed_waves<D>() * kWave),
+                     mixed_plan_lds(p.B), stream, p);
   return (int)hipGetLastError();
 }
 
@@ -1227,22 +1387,13 @@ extern "C" int cie_mixed_trace_buffer(void* buf) {
 }
 #endif
 
-extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, const void* v_pool,
-                                   const int64_t* cu_seqlens, const int64_t* kv_lens,
-                                   const int64_t* slot_ids, const int64_t* block_table,
-                                   void* partials, int64_t partials_bytes, int32_t* counters,
-                                   int64_t B, int64_t total_T,
-                                   int64_t max_seqlen, int64_t H_q, int64_t H_kv, int64_t D,
-                                   int64_t page_size, int64_t n_pages, int64_t pool_page_stride,
-                                   int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
-                                   int64_t n_slots, int32_t* err, void* stream) {
+// Checks of the batch shape shared by the entry points, and the parameters
+// they determine (the budget of partial rows from partials_bytes included).
+static int mixed_shape(MixedParams& p, int64_t B, int64_t total_T, int64_t max_seqlen, int64_t H_q,
+                       int64_t H_kv, int64_t D, int64_t page_size, int64_t bt_width,
+                       int64_t n_slots, int64_t partials_bytes) {
   if (B < 0 || total_T < 0 || max_seqlen < 0 || H_q <= 0 || H_kv <= 0 || H_q % H_kv != 0 ||
-      n_pages <= 0 || bt_width <= 0 || bt_stride < bt_width || n_slots <= 0 || page_size <= 0 ||
-      partials_bytes < 0)
-    return CIE_EINVAL;
-  if (B == 0 || total_T == 0 || max_seqlen == 0) return CIE_OK;
-  if (!o || !q || !k_pool || !v_pool || !cu_seqlens || !kv_lens || !slot_ids || !block_table ||
-      (!partials && partials_bytes > 0) || !counters)
+      bt_width <= 0 || n_slots <= 0 || page_size <= 0 || partials_bytes < 0)
     return CIE_EINVAL;
   const int64_t G = H_q / H_kv;
   const int64_t n_qtiles = (max_seqlen + 15) / 16;
@@ -1257,35 +1408,6 @@ extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, c
       16 * H_q * kMaxChunks * D * 4 > 0x7fffffff)
     return CIE_EUNSUPPORTED;
   if (D != 64 && D != 128) return CIE_EUNSUPPORTED;
-  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(o) |
-       reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool) |
-       reinterpret_cast<uintptr_t>(partials) | reinterpret_cast<uintptr_t>(counters)) & 15)
-    return CIE_EINVAL;
-  if (pool_page_stride % 8 != 0 || pool_head_stride % 8 != 0) return CIE_EINVAL;
-
-  MixedParams p{};
-  p.o = static_cast<f16*>(o);
-  p.q = static_cast<const f16*>(q);
-  p.k_pool = static_cast<const f16*>(k_pool);
-  p.v_pool = static_cast<const f16*>(v_pool);
-  p.cu_seqlens = cu_seqlens;
-  p.kv_lens = kv_lens;
-  p.slot_ids = slot_ids;
-  p.block_table = block_table;
-  // The buffer sets the budget of partial rows: sequences whose split tiles
-  // do not fit run unsplit (the plan's pbase).
-  const int64_t cap = mixed_partial_rows(partials_bytes, D);
-  const MixedLayout w = mixed_layout(cap, D);
-  char* ws = static_cast<char*>(partials);
-  p.part_m = reinterpret_cast<float*>(ws + w.m);
-  p.part_l = reinterpret_cast<float*>(ws + w.l);
-  p.part_acc = reinterpret_cast<float*>(ws + w.acc);
-  p.part_cap = cap;
-  p.counters = counters;
-  p.pool_page_stride = pool_page_stride;
-  p.pool_head_stride = pool_head_stride;
-  p.bt_stride = bt_stride;
-  p.n_pages = n_pages;
   p.total_T = total_T;
   p.bt_width = (int32_t)bt_width;
   p.n_slots = (int32_t)(n_slots > 0x7fffffff ? 0x7fffffff : n_slots);
@@ -1296,11 +1418,141 @@ extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, c
   p.page_size = (int32_t)page_size;
   p.n_qtiles = (int32_t)n_qtiles;
   p.g_magic = div_magic((uint32_t)G);
-  const int64_t pool_bytes = n_pages * pool_page_stride * 2;
-  p.pool_bytes = pool_bytes < ((int64_t)1 << 32) ? (uint32_t)pool_bytes : 0u;
   p.tpp_magic = div_magic((uint32_t)(page_size / 16));
   p.scale_log2 = kLog2e / __builtin_sqrtf((float)D);
+  // The buffer sets the budget of partial rows: sequences whose split tiles
+  // do not fit run unsplit (the plan's pbase).
+  p.part_cap = mixed_partial_rows(partials_bytes, D);
+  return CIE_OK;
+}
+
+// Items a batch can have at most (the plan's capacity): every sequence's
+// query tiles (at most total_T / 16 + B over the batch), each in at most
+// kMaxColGroups column groups of kMaxChunks chunks.
+static int64_t mixed_plan_items(int64_t B, int64_t total_T) {
+  const int64_t n = ((total_T + 15) / 16 + B) * kMaxColGroups * kMaxChunks;
+  const int64_t lim = (0x7fffffff - kPlanHeader) / 8;
+  return n < lim ? n : lim;
+}
+
+// The pointers and pool geometry of an attention launch (planned or not).
+static int mixed_operands(MixedParams& p, void* o, const void* q, const void* k_pool,
+                          const void* v_pool, const int64_t* block_table, void* partials,
+                          int64_t partials_bytes, int32_t* counters, int64_t D, int64_t n_pages,
+                          int64_t pool_page_stride, int64_t pool_head_stride, int64_t bt_stride,
+                          int64_t bt_width) {
+  if (n_pages <= 0 || bt_stride < bt_width) return CIE_EINVAL;
+  if (!o || !q || !k_pool || !v_pool || !block_table || (!partials && partials_bytes > 0) ||
+      !counters)
+    return CIE_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(o) |
+       reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool) |
+       reinterpret_cast<uintptr_t>(partials) | reinterpret_cast<uintptr_t>(counters)) & 15)
+    return CIE_EINVAL;
+  if (pool_page_stride % 8 != 0 || pool_head_stride % 8 != 0) return CIE_EINVAL;
+  p.o = static_cast<f16*>(o);
+  p.q = static_cast<const f16*>(q);
+  p.k_pool = static_cast<const f16*>(k_pool);
+  p.v_pool = static_cast<const f16*>(v_pool);
+  p.block_table = block_table;
+  const MixedLayout w = mixed_layout(p.part_cap, D);
+  char* ws = static_cast<char*>(partials);
+  p.part_m = reinterpret_cast<float*>(ws + w.m);
+  p.part_l = reinterpret_cast<float*>(ws + w.l);
+  p.part_acc = reinterpret_cast<float*>(ws + w.acc);
+  p.counters = counters;
+  p.pool_page_stride = pool_page_stride;
+  p.pool_head_stride = pool_head_stride;
+  p.bt_stride = bt_stride;
+  p.n_pages = n_pages;
+  const int64_t pool_bytes = n_pages * pool_page_stride * 2;
+  p.pool_bytes = pool_bytes < ((int64_t)1 << 32) ? (uint32_t)pool_bytes : 0u;
+  return CIE_OK;
+}
+
+extern "C" int cie_mixed_attention(void* o, const void* q, const void* k_pool, const void* v_pool,
+                                   const int64_t* cu_seqlens, const int64_t* kv_lens,
+                                   const int64_t* slot_ids, const int64_t* block_table,
+                                   void* partials, int64_t partials_bytes, int32_t* counters,
+                                   int64_t B, int64_t total_T,
+                                   int64_t max_seqlen, int64_t H_q, int64_t H_kv, int64_t D,
+                                   int64_t page_size, int64_t n_pages, int64_t pool_page_stride,
+                                   int64_t pool_head_stride, int64_t bt_stride, int64_t bt_width,
+                                   int64_t n_slots, int32_t* err, void* stream) {
+  MixedParams p{};
+  int rc = mixed_shape(p, B, total_T, max_seqlen, H_q, H_kv, D, page_size, bt_width, n_slots,
+                       partials_bytes);
+  if (rc == CIE_EINVAL) return rc;
+  if (n_pages <= 0 || bt_stride < bt_width) return CIE_EINVAL;
+  if (B == 0 || total_T == 0 || max_seqlen == 0) return CIE_OK;
+  if (rc != CIE_OK) return rc;
+  if (!cu_seqlens || !kv_lens || !slot_ids) return CIE_EINVAL;
+  rc = mixed_operands(p, o, q, k_pool, v_pool, block_table, partials, partials_bytes, counters, D,
+                      n_pages, pool_page_stride, pool_head_stride, bt_stride, bt_width);
+  if (rc != CIE_OK) return rc;
+  p.cu_seqlens = cu_seqlens;
+  p.kv_lens = kv_lens;
+  p.slot_ids = slot_ids;
   p.err = err;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return D == 64 ? launch_mixed<64>(p, st) : launch_mixed<128>(p, st);
+  return D == 64 ? launch_mixed<64, false>(p, st) : launch_mixed<128, false>(p, st);
+}
+
+extern "C" int64_t cie_mixed_plan_bytes(int64_t B, int64_t total_T) {
+  if (B < 0 || total_T < 0 || B > kMaxSeqs || total_T > 0x7fffffff) return -1;
+  return (kPlanHeader + 8 * mixed_plan_items(B, total_T)) * (int64_t)sizeof(int32_t);
+}
+
+extern "C" int cie_mixed_plan(int32_t* plan, int64_t plan_bytes, const int64_t* cu_seqlens,
+                              const int64_t* kv_lens, const int64_t* slot_ids, int64_t B,
+                              int64_t total_T, int64_t max_seqlen, int64_t H_q, int64_t H_kv,
+                              int64_t D, int64_t page_size, int64_t bt_width, int64_t n_slots,
+                              int64_t partials_bytes, int32_t* err, void* stream) {
+  MixedParams p{};
+  int rc = mixed_shape(p, B, total_T, max_seqlen, H_q, H_kv, D, page_size, bt_width, n_slots,
+                       partials_bytes);
+  if (rc == CIE_EINVAL) return rc;
+  if (B == 0 || total_T == 0 || max_seqlen == 0) return CIE_OK;  // the planned call does nothing
+  if (rc != CIE_OK) return rc;
+  if (!plan || !cu_seqlens || !kv_lens || !slot_ids || (reinterpret_cast<uintptr_t>(plan) & 15) ||
+      plan_bytes < cie_mixed_plan_bytes(B, total_T))
+    return CIE_EINVAL;
+  p.cu_seqlens = cu_seqlens;
+  p.kv_lens = kv_lens;
+  p.slot_ids = slot_ids;
+  p.plan_out = plan;
+  p.plan_cap = (int32_t)mixed_plan_items(B, total_T);
+  p.err = err;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return D == 64 ? launch_mixed_plan<64>(p, st) : launch_mixed_plan<128>(p, st);
+}
+
+extern "C" int cie_mixed_attention_planned(void* o, const void* q, const void* k_pool,
+                                           const void* v_pool, const int32_t* plan,
+                                           int64_t plan_bytes, const int64_t* block_table,
+                                           void* partials, int64_t partials_bytes,
+                                           int32_t* counters, int64_t B, int64_t total_T,
+                                           int64_t max_seqlen, int64_t H_q, int64_t H_kv,
+                                           int64_t D, int64_t page_size, int64_t n_pages,
+                                           int64_t pool_page_stride, int64_t pool_head_stride,
+                                           int64_t bt_stride, int64_t bt_width, int64_t n_slots,
+                                           int32_t* err, void* stream) {
+  MixedParams p{};
+  int rc = mixed_shape(p, B, total_T, max_seqlen, H_q, H_kv, D, page_size, bt_width, n_slots,
+                       partials_bytes);
+  if (rc == CIE_EINVAL) return rc;
+  if (n_pages <= 0 || bt_stride < bt_width) return CIE_EINVAL;
+  if (B == 0 || total_T == 0 || max_seqlen == 0) return CIE_OK;
+  if (rc != CIE_OK) return rc;
+  if (!plan || (reinterpret_cast<uintptr_t>(plan) & 15) ||
+      plan_bytes < cie_mixed_plan_bytes(B, total_T))
+    return CIE_EINVAL;
+  rc = mixed_operands(p, o, q, k_pool, v_pool, block_table, partials, partials_bytes, counters, D,
+                      n_pages, pool_page_stride, pool_head_stride, bt_stride, bt_width);
+  if (rc != CIE_OK) return rc;
+  p.plan = plan;
+  p.plan_cap = (int32_t)mixed_plan_items(B, total_T);
+  p.err = err;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return D == 64 ? launch_mixed<64, true>(p, st) : launch_mixed<128, true>(p, st);
 }

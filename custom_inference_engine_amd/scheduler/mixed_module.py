@@ -44,6 +44,7 @@ import contextlib
 
 import torch
 
+from ..attn.core import gqa_mixed_plan_op
 from ..attn.metadata import AttentionMetadata
 from ..graphs import StepGraph, StepInputs
 from ..piecewise import get_piecewise_backend
@@ -87,6 +88,14 @@ class MixedModule:
         self.positions.copy_(pos)
         self.metadata.pages.copy_(torch.where(live, kv.block_table[slot, pos // kv.page_size], 0))
         self.metadata.offsets.copy_(pos % kv.page_size)
+        # one plan for every layer's mixed attention: the step's sequences are
+        # the same for all of them (the lengths advance after the step).  (A
+        # step prepared on the CPU — traced, never run — has none.)
+        if kv.keys[0].is_cuda:
+            T = self.token_count
+            self.metadata.mixed_plan = gqa_mixed_plan_op(
+                kv.keys[0], self.cu_seqlens, kv.lens[self.slots], self.slots, kv.block_table, T, T,
+                self.model.config.num_attention_heads)
 
     def _forward(self) -> torch.Tensor:
         return self.model.model(input_ids=self.tokens[None], position_ids=self.positions[None],

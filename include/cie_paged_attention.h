@@ -43,6 +43,10 @@ extern "C" {
 #define CIE_ERRBIT_OFFSET 4   /* in-page offset outside [0, page_size)           */
 #define CIE_ERRBIT_SPLIT 8    /* a split-arrival counter held a stale value at the
                                  start of the call (see `counters` below)        */
+#define CIE_ERRBIT_PLAN 16    /* a planned call whose plan was made for another
+                                 batch shape or partials budget (the call wrote
+                                 nothing), or a batch with more work items than
+                                 its plan holds (cie_mixed_plan)                  */
 
 /* Version of this ABI (bumped on any signature change). */
 int cie_abi_version(void);
@@ -352,6 +356,48 @@ int cie_mixed_attention(void* o, const void* q,
                         int64_t pool_page_stride, int64_t pool_head_stride,
                         int64_t bt_stride, int64_t bt_width, int64_t n_slots,
                         int32_t* err, void* stream);
+
+/*
+ * Planned mixed attention: one plan per mixed step.  The batch's sequences
+ * (cu_seqlens, kv_lens, slot_ids) are the same for every layer of a step, as
+ * the reference's AttentionMetadata is built once per step
+ * (attn/metadata.py:3-55) and every layer's mixed_gqa_attention reads it
+ * (attn/core.py:69-111).  cie_mixed_plan runs the plan each launch of
+ * cie_mixed_attention makes for itself — the work items, their order and
+ * the sequences' partial bases — once, into `plan`; each layer's
+ * cie_mixed_attention_planned then reads its items' descriptors in one
+ * memory round trip instead of loading the sequence tables and planning.
+ * The results equal cie_mixed_attention's bit for bit.
+ *   plan          : cie_mixed_plan_bytes(B, total_T) bytes, 16-byte aligned;
+ *                   valid for the batch (cu_seqlens, kv_lens, slot_ids),
+ *                   shape and partials_bytes it was made with.  A planned
+ *                   call whose B, max_seqlen's query tiles, H_q, H_kv or
+ *                   partials budget differ from the plan's writes nothing
+ *                   and raises CIE_ERRBIT_PLAN.  A batch with more items than
+ *                   the plan holds (only sequences that overlap in
+ *                   cu_seqlens can have them) gets an empty plan and
+ *                   CIE_ERRBIT_PLAN.  Rows past max_seqlen are reported
+ *                   (CIE_ERRBIT_LEN) by cie_mixed_plan.
+ *   other arguments as for cie_mixed_attention.
+ */
+int64_t cie_mixed_plan_bytes(int64_t B, int64_t total_T);
+int cie_mixed_plan(int32_t* plan, int64_t plan_bytes,
+                   const int64_t* cu_seqlens, const int64_t* kv_lens, const int64_t* slot_ids,
+                   int64_t B, int64_t total_T, int64_t max_seqlen,
+                   int64_t H_q, int64_t H_kv, int64_t D, int64_t page_size,
+                   int64_t bt_width, int64_t n_slots, int64_t partials_bytes,
+                   int32_t* err, void* stream);
+int cie_mixed_attention_planned(void* o, const void* q,
+                                const void* k_pool, const void* v_pool,
+                                const int32_t* plan, int64_t plan_bytes,
+                                const int64_t* block_table,
+                                void* partials, int64_t partials_bytes, int32_t* counters,
+                                int64_t B, int64_t total_T, int64_t max_seqlen,
+                                int64_t H_q, int64_t H_kv, int64_t D,
+                                int64_t page_size, int64_t n_pages,
+                                int64_t pool_page_stride, int64_t pool_head_stride,
+                                int64_t bt_stride, int64_t bt_width, int64_t n_slots,
+                                int32_t* err, void* stream);
 
 #ifdef __cplusplus
 }
