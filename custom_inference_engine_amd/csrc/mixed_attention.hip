@@ -27,8 +27,11 @@
 // tile and column group) merges them with log-sum-exp, writes o and resets
 // the counter.  Partials are packed per launch: only split tiles have rows,
 // sequence by sequence, within a budget the caller's buffer sets; a
-// sequence past it runs unsplit (see the tile runs below).  The reference instead walks a tile's whole prefix with one
-// program and pads every L = 1 sequence to a 16-row tile
+// sequence past it runs unsplit (see the tile runs below).  Every workgroup
+// plans the batch (item counts, dealing order, partial bases) at its start;
+// a planned launch reads that plan, made once per mixed step by
+// mixed_plan_kernel, instead.  The reference instead walks a tile's whole
+// prefix with one program and pads every L = 1 sequence to a 16-row tile
 // (prefill_attention.py:49-50, 93).
 #include "attn_engine.h"
 
