@@ -70,6 +70,8 @@ def parse():
                     help="phase trace of one config-2 call; needs a trace build of the library "
                          "(python -m custom_inference_engine_amd._build -D CIE_DECODE_TRACE --out DIR, "
                          "then --lib DIR/libcie_paged.so)")
+    ap.add_argument("--trace-planned", action="store_true",
+                    help="with --trace-mixed: trace planned launches (the step's plan made once)")
     ap.add_argument("--trace-mixed", action="store_true",
                     help="per-item phase trace of one config-3 mixed launch (--config 6: the feature "
                          "bench's B = 1 shape); needs a trace build (-D CIE_MIXED_TRACE, then --lib)")
@@ -410,10 +412,13 @@ def trace_mixed(args):
     buf = torch.zeros(2 * 4096 * 16, dtype=torch.int64, device=dev)
     if lib.cie_mixed_trace_buffer(buf.data_ptr()) != 0:
         raise SystemExit("cie_mixed_trace_buffer failed")
+    plan = (cie.mixed_plan(pools[0][0], c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table, max_seqlen, case.T,
+                           case.q.shape[2]) if args.trace_planned else None)
     for it in range(3 * R):
         kp, vp = pools[it % R]
         buf.zero_()
-        cie.mixed_gqa_attention(c.q, kp, vp, max_seqlen, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table)
+        cie.mixed_gqa_attention(c.q, kp, vp, max_seqlen, c.cu_seqlens, c.kv_lens, c.slot_ids, c.block_table,
+                                plan=plan)
     torch.cuda.synchronize()
     lib.cie_mixed_trace_buffer(None)
     t = buf.view(2, 4096, 16).cpu()
