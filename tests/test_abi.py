@@ -223,3 +223,40 @@ def test_plan_rejects_what_it_cannot_hold(native_lib):
     assert lib.cie_paged_decode_plan_workgroups(4, 2, 65) == -1
     assert lib.cie_paged_decode_plan_workgroups(4, 2, 16) == 128
     assert lib.cie_paged_decode_plan_bytes(256) == 256 * (8 + 4 * 64) * 4
+
+
+def test_mixed_plan_rejects_bad_arguments_without_launching(native_lib):
+    """cie_mixed_plan / cie_mixed_attention_planned check sizes and pointers on
+    the host (fake addresses, never read)."""
+    lib = native_lib
+    need = lib.cie_mixed_plan_bytes(4, 100)
+    # header + 8 words per item, room for every item of 100 tokens in 4 sequences:
+    # (ceil(100/16) + 4) tiles x 8 column groups x 16 chunks
+    assert need == (8 + 8 * (7 + 4) * 8 * 16) * 4
+    assert lib.cie_mixed_plan_bytes(0, 0) == 32
+    assert lib.cie_mixed_plan_bytes(-1, 100) == -1 and lib.cie_mixed_plan_bytes(1025, 100) == -1
+
+    def plan(**over):
+        a = dict(plan=4096, plan_bytes=need, cu=16, kvl=32, slots=48, B=4, T=100, ms=40, H_q=14, H_kv=2, D=64,
+                 ps=16, bt_width=64, n_slots=8, pbytes=0)
+        a.update(over)
+        return lib.cie_mixed_plan(a["plan"], a["plan_bytes"], a["cu"], a["kvl"], a["slots"], a["B"], a["T"],
+                                  a["ms"], a["H_q"], a["H_kv"], a["D"], a["ps"], a["bt_width"], a["n_slots"],
+                                  a["pbytes"], None, None)
+    assert plan(plan_bytes=need - 4) == -1      # too small for the batch's items
+    assert plan(plan=None) == -1
+    assert plan(plan=4104) == -1                # not 16-byte aligned
+    assert plan(pbytes=-1) == -1
+    assert plan(B=1025, plan_bytes=1 << 30) == -2  # more sequences than a launch plans
+    assert plan(H_q=14, H_kv=1) == -2           # G = 14 is outside the built set
+    assert plan(B=0) == 0 and plan(T=0) == 0    # empty batch: nothing to plan
+
+    def planned(**over):
+        a = dict(plan=4096, plan_bytes=need, counters=8192)
+        a.update(over)
+        return lib.cie_mixed_attention_planned(16, 16, 16, 16, a["plan"], a["plan_bytes"], 8, None, 0,
+                                               a["counters"], 4, 100, 40, 14, 2, 64, 16, 64, 1024, 1024,
+                                               64, 64, 8, None, None)
+    assert planned(plan=None) == -1
+    assert planned(plan_bytes=need - 4) == -1
+    assert planned(counters=None) == -1
