@@ -71,7 +71,7 @@ def parse():
                          "(python -m custom_inference_engine_amd._build -D CIE_DECODE_TRACE --out DIR, "
                          "then --lib DIR/libcie_paged.so)")
     ap.add_argument("--trace-planned", action="store_true",
-                    help="with --trace-mixed: trace planned launches (the step's plan made once)")
+                    help="with --trace-mixed / --trace-decode: trace planned launches (the step's plan made once)")
     ap.add_argument("--trace-mixed", action="store_true",
                     help="per-item phase trace of one config-3 mixed launch (--config 6: the feature "
                          "bench's B = 1 shape); needs a trace build (-D CIE_MIXED_TRACE, then --lib)")
@@ -341,17 +341,21 @@ def trace_decode(args):
     W, slots = 4, 24
     R = max(1, -(-MIN_ROTATION_BYTES // (2 * case.k_pool.numel() * 2)))
     pools = [(c.k_pool.clone(), c.v_pool.clone()) for _ in range(R)]
-    buf = torch.zeros(case.B * 2 * S * slots, dtype=torch.int64, device=dev)
+    plan = (cie.decode_plan(pools[0][0], c.lens_pool, c.slot_ids, c.block_table, append=True, num_programs=S)
+            if args.trace_planned else None)
+    n_wg = plan.numel() // cie.attn.core.PLAN_WORDS_PER_WORKGROUP if plan is not None else case.B * 2 * S
+    buf = torch.zeros(max(n_wg, case.B * 2 * S) * slots, dtype=torch.int64, device=dev)
     if lib.cie_decode_trace_buffer(buf.data_ptr()) != 0:
         raise SystemExit("cie_decode_trace_buffer failed")
     for it in range(3 * R):
         kp, vp = pools[it % R]
         buf.zero_()
         cie.decode_append_gqa_attention(c.q, kp, vp, c.k_new, c.v_new, c.lens_pool, c.slot_ids,
-                                        c.block_table, num_programs=S)
+                                        c.block_table, num_programs=None if plan is not None else S, plan=plan)
     torch.cuda.synchronize()
     lib.cie_decode_trace_buffer(None)
     t = buf.view(-1, slots).cpu()
+    t = t[t[:, 0] != 0]  # workgroups that ran (a plan may leave some idle)
     t0 = t[:, 0].min().item()
 
     def us(v):
@@ -371,7 +375,7 @@ def trace_decode(args):
         by_xcd[int(t[r, 6].item()) & 0xF].append(ends[r])
     print("loop end by XCD (median/max): " + "  ".join(
         f"{x}:{statistics.median(v):.2f}/{max(v):.2f}" for x, v in sorted(by_xcd.items())))
-    for sp in range(S):
+    for sp in range(0 if plan is not None else S):
         rows = [r for r in range(t.shape[0]) if r % S == sp]
         for w in range(W):
             first = [us(t[r, 20 + w].item()) for r in rows if t[r, 20 + w].item()]
