@@ -479,13 +479,17 @@ __device__ __forceinline__ void stream_tiles(SoftmaxAcc<D, NCT>& st, const QS& q
 // reference-max check on S(t), then P(t) = 2^(S(t)*scale - m) and
 // acc += V(t)^T . P(t)^T.  stream_tiles_pipelined puts step t's softmax and
 // P.V and step t+1's S MFMAs in one basic block (they depend on nothing in
-// each other), one MFMA issued between every three VALU instructions; the
+// each other), in segments of one column tile each (step_segment); the
 // masking and reference-max check of step t+1 follow in their own short
-// blocks, the rare rescale in a branch.  (A lone wave on a gfx950 SIMD
-// overlaps its own MFMA and VALU work only in part — measured: a step's
-// math alone costs about the sum of its MFMA and VALU parts — so this
-// schedule gains little by itself; the stream's one-descriptor loads gain
-// more.)
+// blocks, the rare rescale in a branch.
+//
+// The step is VALU-bound on one wave: measured on gfx950 (timing kernels on
+// register operands), its 32 MFMAs take ~525 cycles and its softmax VALU
+// work alone ~930, half of that the 32 v_exp_f32 (a transcendental: ~16
+// cycles each for one wave).  A wave keeps issuing while its MFMA runs, so an
+// MFMA followed by one exponential costs ~20 cycles instead of 16 + 16; the
+// segments pair them one to one (the whole step's math: ~1,150 cycles
+// instead of ~1,315 with the compiler's own interleave).
 
 // S^T of one step against column tile c: s[t] = K(tile t) . Q(c)^T.
 template <int D, class QS>
@@ -559,50 +563,49 @@ __device__ __forceinline__ void v_operands(f16x8 (&va)[Geo<D>::NT], const KVPair
     for (int e = 0; e < 8; ++e) va[nt][e] = kv.v[e][nt];
 }
 
-// S^T of one step against one column tile whose Q^T operands are in q.
-template <int D>
-__device__ __forceinline__ void tile_scores_q(f32x4 (&s)[2], const KVPair<D>& kv,
-                                              const f16x8 (&q)[Geo<D>::KS]) {
-  s[0] = f32x4{0.f, 0.f, 0.f, 0.f};
-  s[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ks = 0; ks < Geo<D>::KS; ++ks) {
-    s[0] = mfma16x16x32(kv.k[0][ks], q[ks], s[0]);
-    s[1] = mfma16x16x32(kv.k[1][ks], q[ks], s[1]);
-  }
-}
-
-// P = 2^(s * scale - m) of one column tile, in fp16 (the P.V operand).
-__device__ __forceinline__ f16x8 tile_probs(float m, const f32x4 (&s)[2], float scale_log2) {
-  f16x8 pop;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    pop[r] = (f16)fast_exp2(__builtin_fmaf(s[0][r], scale_log2, -m));
-    pop[4 + r] = (f16)fast_exp2(__builtin_fmaf(s[1][r], scale_log2, -m));
-  }
-  return pop;
-}
-
-// acc += V^T . P^T of column tile c, and the lane's part of the row sums
-// += its 8 fp16 P values (v_dot2_f32_f16 against (1, 1): exact products,
-// fp32 sums; one register a column tile instead of an MFMA output's four).
+// One segment of a pipelined step: for column tile c (c < NCT) its
+// exponentials and the S MFMAs of its next step's scores, and for tile c - 1
+// (c > 0) its P.V MFMAs.  The P.V and S MFMAs alternate (NT of each), and
+// exponential r of tile c follows MFMA r * 2 * NT / 8, so each MFMA runs
+// while the wave issues one exponential (D = 64; every second MFMA for
+// D = 128).  The scheduling barriers keep the compiler from regrouping them
+// (its own interleave puts the eight exponentials of a tile back to back).
+// x: 2^x arguments of tile c (s * scale - m); e: the exponentials.
 template <int D, int NCT>
-__device__ __forceinline__ void accumulate_probs(SoftmaxAcc<D, NCT>& st, int c, const f16x8& pop,
-                                                 const f16x8 (&va)[Geo<D>::NT]) {
+__device__ __forceinline__ void step_segment(SoftmaxAcc<D, NCT>& st, int c, const f16x8& pprev,
+                                             const f16x8 (&va)[Geo<D>::NT], const KVPair<D>& kv,
+                                             const f16x8 (&q)[Geo<D>::KS], f32x4 (&s1)[2],
+                                             const float (&x)[8], float (&e)[8]) {
+  constexpr int NT = Geo<D>::NT;
+  constexpr int NM = 2 * NT;  // NT P.V MFMAs and 2 * KS = NT S MFMAs
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    const int j = i / 2;
+    if (i % 2 == 0) {
+      if (c > 0) st.acc[c - 1][j] = mfma16x16x32(va[j], pprev, st.acc[c - 1][j]);
+    } else if (c < NCT) {
+      // S(t = j % 2, k-step j / 2): a tile's two k-steps are 4 MFMAs apart
+      const int t = j % 2, ks = j / 2;
+      s1[t] = mfma16x16x32(kv.k[t][ks], q[ks], ks == 0 ? zero : s1[t]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (c < NCT && (i * 8) % NM == 0) e[i * 8 / NM] = fast_exp2(x[i * 8 / NM]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// The lane's part of column tile c's row sums += its 8 fp16 P values
+// (v_dot2_f32_f16 against (1, 1): exact products, fp32 sums; one register a
+// column tile instead of an MFMA output's four).
+__device__ __forceinline__ void add_row_sums(float& lpart, const f16x8& p) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const h2 one2 = {(f16)1.f, (f16)1.f};
+  float l = lpart;
 #pragma unroll
-  for (int nt = 0; nt < Geo<D>::NT; ++nt) st.acc[c][nt] = mfma16x16x32(va[nt], pop, st.acc[c][nt]);
-  float l = st.lpart[c];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) l = __builtin_amdgcn_fdot2(h2{pop[2 * i], pop[2 * i + 1]}, one2, l, false);
-  st.lpart[c] = l;
+  for (int i = 0; i < 4; ++i) l = __builtin_amdgcn_fdot2(h2{p[2 * i], p[2 * i + 1]}, one2, l, false);
+  lpart = l;
 }
-
-// 1: interleave each segment's MFMAs one at a time with its VALU work
-#ifndef CIE_STEP_INTERLEAVE
-#define CIE_STEP_INTERLEAVE 1
-#endif
 
 // stream_tiles with steps overlapped as described above.  Step t's V rows
 // are loaded at the start of step t-1 and its K tiles at the start of step
@@ -732,31 +735,28 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
           // Segment c: the exponentials of column tile c, the P.V MFMAs of
           // tile c - 1 and the S MFMAs of tile c for the next step.
           // Scheduling barriers between segments keep each step's scores
-          // consumed as the next step's are produced (registers); inside a
-          // segment the MFMAs are issued one at a time between VALU
-          // instructions.
+          // consumed as the next step's are produced (registers).
           f32x4 s1[NCT][2];
           f16x8 pprev;
 #pragma unroll
           for (int c = 0; c <= NCT; ++c) {
             __builtin_amdgcn_sched_barrier(0);
             f16x8 q[Geo<D>::KS];
+            float x[8], e[8];
             if (c < NCT) {
 #pragma unroll
               for (int ks = 0; ks < Geo<D>::KS; ++ks) q[ks] = qop(c, ks);
-            }
-            f16x8 pc;
-            if (c < NCT) pc = tile_probs(st.m[c], s[c], scale_log2);
-            if (c > 0) accumulate_probs<D, NCT>(st, c - 1, pprev, va);
-            if (c < NCT) tile_scores_q<D>(s1[c], ring[(u + 1) % 3], q);
-            pprev = pc;
-            if (CIE_STEP_INTERLEAVE && c > 0 && c < NCT) {
-              __builtin_amdgcn_sched_group_barrier(0x100, 2 * Geo<D>::KS, 0);  // Q reads
 #pragma unroll
-              for (int i = 0; i < NT + 2 * Geo<D>::KS; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+              for (int r = 0; r < 4; ++r) {
+                x[r] = __builtin_fmaf(s[c][0][r], scale_log2, -st.m[c]);
+                x[4 + r] = __builtin_fmaf(s[c][1][r], scale_log2, -st.m[c]);
               }
+            }
+            step_segment<D, NCT>(st, c, pprev, va, ring[(u + 1) % 3], q, s1[c < NCT ? c : 0], x, e);
+            if (c > 0) add_row_sums(st.lpart[c - 1], pprev);
+            if (c < NCT) {
+#pragma unroll
+              for (int r = 0; r < 8; ++r) pprev[r] = (f16)e[r];
             }
           }
           __builtin_amdgcn_sched_barrier(0);
