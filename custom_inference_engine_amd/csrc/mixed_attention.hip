@@ -45,7 +45,9 @@ namespace cie {
 //   CIE_MIXED_NARROW_PAIRS the same for a tile of one column tile (a decode
 //                          row: its steps are cheap, its keys many, so it is
 //                          split sooner and its chunks spread over idle
-//                          workgroups)
+//                          workgroups; 12 measured faster than 8, 16 or 32
+//                          at config 3: a chunk's fixed cost, not its few
+//                          steps, sets its time)
 //   CIE_MIXED_PF           32-key steps of loads in flight per wave (D = 64)
 //   CIE_MIXED_QLDS         1: the item's Q operands live in LDS (one copy per
 //                          workgroup), not registers (a wave then fits 256
@@ -79,7 +81,7 @@ namespace cie {
 #define CIE_MIXED_PIPELINED 1
 #endif
 #ifndef CIE_MIXED_NARROW_PAIRS
-#define CIE_MIXED_NARROW_PAIRS 8
+#define CIE_MIXED_NARROW_PAIRS 12
 #endif
 #ifndef CIE_MIXED_NARROW_PF
 #define CIE_MIXED_NARROW_PF 1

@@ -342,8 +342,8 @@ def test_mixed_counters_preloaded_negative_are_flagged_then_reset(native_lib):
 def _split_partial_rows(prior, new, h_q, h_kv, n_qtiles):
     """Partial rows each sequence's split tiles take, tile by tile: a tile of
     `rows` rows with k >= 2 chunks holds rows * H_q * k; k = clamp(ceil(pairs
-    / per), 1, 16) for the tile's 32-key steps, per = 4 waves x 8 steps (one
-    column tile) or 4 x 24 (wider)."""
+    / per), 1, 16) for the tile's 32-key steps, per = 4 waves x 12 steps (one
+    column tile: CIE_MIXED_NARROW_PAIRS) or 4 x 24 (wider)."""
     G = h_q // h_kv
     out = []
     for c, L in zip(prior, new):
@@ -352,7 +352,7 @@ def _split_partial_rows(prior, new, h_q, h_kv, n_qtiles):
             rows = min(16, L - 16 * t)
             n_ctiles = (rows * G + 15) // 16
             pairs = ((c + 16 * t + rows + 15) // 16 + 1) // 2
-            per = 4 * 8 if n_ctiles == 1 else 4 * 24
+            per = 4 * 12 if n_ctiles == 1 else 4 * 24
             k = max(1, min(16, -(-pairs // per)))
             if k > 1:
                 r += rows * h_q * k
@@ -397,14 +397,14 @@ def _written_m_rows(ws, cap):
 
 
 def test_mixed_partials_config3_default_budget(native_lib):
-    """Config 3 takes 784 partial rows (its decode rows split, its prefill
+    """Config 3 takes 504 partial rows (its decode rows split, its prefill
     chunks do not), well inside the default budget (2 rows per token and
-    head, under 8 MB): the call writes exactly rows [0, 784) of part_m,
+    head, under 8 MB): the call writes exactly rows [0, 504) of part_m,
     nothing past its buffer, and matches the oracle."""
     case = inputs.config3()
     ms = case.meta["max_seqlen"]
     need = _split_partial_rows(case.kv_lens.tolist(), case.new_lens.tolist(), 14, 2, (ms + 15) // 16)
-    assert sum(need) == 784
+    assert sum(need) == 504
     nbytes = _native.load().cie_mixed_partials_bytes(case.T, 14, 64)
     assert nbytes <= 8_000_000
     note(f"mixed config3 default partials budget ({nbytes} bytes)")
@@ -412,7 +412,7 @@ def test_mixed_partials_config3_default_budget(native_lib):
     assert canary and clean
     cap = (nbytes - 768) // (4 * 66)
     rows = _written_m_rows(ws, cap)
-    assert rows.numel() == 784 and int(rows.max()) == 783
+    assert rows.numel() == 504 and int(rows.max()) == 503
     _check(case, o, "config3, default partials budget")
 
 
@@ -428,7 +428,7 @@ def test_mixed_partials_budget_splits_a_prefix_of_the_batch(native_lib, B):
     prior = torch.randint(0, 3000, (B,), generator=g).tolist()
     new = [int(x) for x in torch.randint(1, 3, (B,), generator=g)]
     prior[2], new[2] = 9000, 20      # a prefill tail whose tiles split
-    prior[5], new[5] = 20000, 1      # a decode row of 16 chunks
+    prior[5], new[5] = 30000, 1      # a decode row of 16 chunks (the cap)
     new[7] = 0                       # an empty sequence
     case = inputs.make_case(prior, new, seed=47 + B)
     ms = int(max(new))
