@@ -647,10 +647,22 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
   const TileLaneOffsets<D> lanes(r16, grp);
   const __amdgpu_buffer_rsrc_t kd = coherent_rsrc(src.k_pool, src.pool_bytes);
   const __amdgpu_buffer_rsrc_t vd = coherent_rsrc(src.v_pool, src.pool_bytes);
-  auto lane_pages = [&](int c0) { return lane_page_id(src, c0, t_end, lane); };
-  // byte offset in the pool of tile c0 + lane (page, head and in-page rows)
+  // Tile c0 + lane of the chunk at c0, or its last tile for lanes past it:
+  // lane ka + 1 then always holds a step's second tile (the last tile again
+  // when it is missing: its keys masked, its V rows zeroed), with no
+  // cross-lane step (the extra page-id loads hit the same lines).
+  auto lane_tile = [&](int c0) { return c0 + min(lane, t_end - c0 - 1); };
+  auto lane_pages = [&](int c0) {
+    int64_t pg = src.bt_row[magic_div(lane_tile(c0), src.tpp_magic)];
+    if (pg < 0 || pg >= src.n_pages) {
+      set_err(src.err, CIE_ERRBIT_PAGE);
+      pg = 0;
+    }
+    return (int)pg;
+  };
+  // byte offset in the pool of that tile (page, head and in-page rows)
   auto lane_offsets = [&](int c0, int page) {
-    const int t = c0 + lane;
+    const int t = lane_tile(c0);
     const int in_page = t - magic_div(t, src.tpp_magic) * tpp;
     return (uint32_t)(((int64_t)page * src.page_stride + src.head_off + (int64_t)(in_page * 16) * D) * 2);
   };
@@ -661,13 +673,27 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
     if (c0 != t_begin) page = lane_pages(c0);
     const uint32_t toff = lane_offsets(c0, page);
     const int n_pairs = (n_chunk + 1) >> 1;
+    // The first steps that need masking (a key at or past some column's
+    // limit, or a missing second tile) and V-row zeroing (a key at or past
+    // key_end): both conditions only grow with the step, so each step tests
+    // one scalar instead of recomputing its keys.  Step j < n_pairs holds
+    // keys [16 * (c0 + 2j), + 32), so it needs masking iff
+    // 16 * (c0 + 2j) + 32 > mask_from (the same with key_end), or its
+    // second tile is missing (2j + 1 == n_chunk).
+    auto first_step_past = [&](int limit) {
+      const int x = limit - 32 - 16 * c0;  // in int range: keys < 2^31 - 32
+      int j = x < 0 ? 0 : x / 32 + 1;
+      if (n_chunk & 1) j = min(j, n_pairs - 1);
+      return uniform(j);
+    };
+    const int j_mask = first_step_past(mask_from);
+    const int j_tail = first_step_past(key_end);
     KVPair<D> ring[3];  // K in slot t % 3, V in slot t % 2
-    // byte offsets of step j's two tiles (a missing second tile: the first
-    // again, its keys masked and its V rows zeroed)
+    // byte offsets of step j's two tiles
     auto offsets = [&](int j, uint32_t& oa, uint32_t& ob) {
       const int ka = 2 * min(j, n_pairs - 1);
       oa = __builtin_amdgcn_readlane(toff, ka);
-      ob = ka + 1 < n_chunk ? __builtin_amdgcn_readlane(toff, ka + 1) : oa;
+      ob = __builtin_amdgcn_readlane(toff, ka + 1);
     };
     // (the lane offsets pass through an empty asm at each use, so the
     // compiler cannot hoist "offset + constant" out of the loop into extra
@@ -712,10 +738,10 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
     f32x4 s[NCT][2];
 #pragma unroll
     for (int c = 0; c < NCT; ++c) tile_scores<D>(s[c], ring[0], qop, c);
-    {
+    if (j_mask == 0) {
       int ka, kb;
       step_keys(0, ka, kb);
-      if (max(ka, kb) + 16 > mask_from) mask_scores<NCT>(s, ka, kb, lim, grp);
+      mask_scores<NCT>(s, ka, kb, lim, grp);
     }
     update_max<D, NCT>(st, s, scale_log2);
     for (int j0 = 0; j0 < n_pairs; j0 += 6) {
@@ -723,10 +749,10 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
       for (int u = 0; u < 6; ++u) {
         const int j = j0 + u;
         if (j < n_pairs) {
-          {
+          if (j >= j_tail) {
             int ka, kb;
             step_keys(j, ka, kb);
-            if (max(ka, kb) + 16 > key_end) zero_tail_rows<D>(ring[u % 2], ka, kb, key_end, grp);
+            zero_tail_rows<D>(ring[u % 2], ka, kb, key_end, grp);
           }
           f16x8 va[NT];
           v_operands<D>(va, ring[u % 2]);
@@ -761,9 +787,11 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
           }
           __builtin_amdgcn_sched_barrier(0);
           if (j + 1 < n_pairs) {
-            int ka, kb;
-            step_keys(j + 1, ka, kb);
-            if (max(ka, kb) + 16 > mask_from) mask_scores<NCT>(s1, ka, kb, lim, grp);
+            if (j + 1 >= j_mask) {
+              int ka, kb;
+              step_keys(j + 1, ka, kb);
+              mask_scores<NCT>(s1, ka, kb, lim, grp);
+            }
             update_max<D, NCT>(st, s1, scale_log2);
           }
 #pragma unroll
