@@ -565,32 +565,38 @@ __device__ __forceinline__ void v_operands(f16x8 (&va)[Geo<D>::NT], const KVPair
 
 // One segment of a pipelined step: for column tile c (c < NCT) its
 // exponentials and the S MFMAs of its next step's scores, and for tile c - 1
-// (c > 0) its P.V MFMAs.  The P.V and S MFMAs alternate (NT of each), and
-// exponential r of tile c follows MFMA r * 2 * NT / 8, so each MFMA runs
+// (c > 0) its P.V MFMAs.  The NT S MFMAs go first, then the NT P.V MFMAs,
+// and exponential r of tile c follows MFMA r * 2 * NT / 8, so each MFMA runs
 // while the wave issues one exponential (D = 64; every second MFMA for
 // D = 128).  The scheduling barriers keep the compiler from regrouping them
 // (its own interleave puts the eight exponentials of a tile back to back).
+// With the S MFMAs first, the Q^T operands q are free after them:
+// next_q(q) then reads the next column tile's into the same registers, a
+// segment's worth of P.V MFMAs ahead of their use (reading them at the
+// segment's start stalled each segment on the LDS round trip).
 // x: 2^x arguments of tile c (s * scale - m); e: the exponentials.
-template <int D, int NCT>
+template <int D, int NCT, class NextQ>
 __device__ __forceinline__ void step_segment(SoftmaxAcc<D, NCT>& st, int c, const f16x8& pprev,
                                              const f16x8 (&va)[Geo<D>::NT], const KVPair<D>& kv,
-                                             const f16x8 (&q)[Geo<D>::KS], f32x4 (&s1)[2],
-                                             const float (&x)[8], float (&e)[8]) {
+                                             f16x8 (&q)[Geo<D>::KS], f32x4 (&s1)[2],
+                                             const float (&x)[8], float (&e)[8], NextQ next_q) {
   constexpr int NT = Geo<D>::NT;
-  constexpr int NM = 2 * NT;  // NT P.V MFMAs and 2 * KS = NT S MFMAs
+  constexpr int NM = 2 * NT;  // 2 * KS = NT S MFMAs, then NT P.V MFMAs
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < NM; ++i) {
-    const int j = i / 2;
-    if (i % 2 == 0) {
-      if (c > 0) st.acc[c - 1][j] = mfma16x16x32(va[j], pprev, st.acc[c - 1][j]);
-    } else if (c < NCT) {
-      // S(t = j % 2, k-step j / 2): a tile's two k-steps are 4 MFMAs apart
-      const int t = j % 2, ks = j / 2;
-      s1[t] = mfma16x16x32(kv.k[t][ks], q[ks], ks == 0 ? zero : s1[t]);
+    if (i < NT) {
+      if (c < NCT) {
+        // S(t = i % 2, k-step i / 2): a tile's k-steps are 2 MFMAs apart
+        const int t = i % 2, ks = i / 2;
+        s1[t] = mfma16x16x32(kv.k[t][ks], q[ks], ks == 0 ? zero : s1[t]);
+      }
+    } else if (c > 0) {
+      st.acc[c - 1][i - NT] = mfma16x16x32(va[i - NT], pprev, st.acc[c - 1][i - NT]);
     }
     __builtin_amdgcn_sched_barrier(0);
     if (c < NCT && (i * 8) % NM == 0) e[i * 8 / NM] = fast_exp2(x[i * 8 / NM]);
+    if (c < NCT && i == NT + 1) next_q(q);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -744,6 +750,10 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
       mask_scores<NCT>(s, ka, kb, lim, grp);
     }
     update_max<D, NCT>(st, s, scale_log2);
+    // Q^T operands of the next segment's column tile (carried across steps)
+    f16x8 q[Geo<D>::KS];
+#pragma unroll
+    for (int ks = 0; ks < Geo<D>::KS; ++ks) q[ks] = qop(0, ks);
     for (int j0 = 0; j0 < n_pairs; j0 += 6) {
 #pragma unroll
       for (int u = 0; u < 6; ++u) {
@@ -767,18 +777,21 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
 #pragma unroll
           for (int c = 0; c <= NCT; ++c) {
             __builtin_amdgcn_sched_barrier(0);
-            f16x8 q[Geo<D>::KS];
             float x[8], e[8];
             if (c < NCT) {
-#pragma unroll
-              for (int ks = 0; ks < Geo<D>::KS; ++ks) q[ks] = qop(c, ks);
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 x[r] = __builtin_fmaf(s[c][0][r], scale_log2, -st.m[c]);
                 x[4 + r] = __builtin_fmaf(s[c][1][r], scale_log2, -st.m[c]);
               }
             }
-            step_segment<D, NCT>(st, c, pprev, va, ring[(u + 1) % 3], q, s1[c < NCT ? c : 0], x, e);
+            // (tile c + 1's Q^T operands, or tile 0's for the next step)
+            auto next_q = [&](f16x8 (&qq)[Geo<D>::KS]) {
+#pragma unroll
+              for (int ks = 0; ks < Geo<D>::KS; ++ks) qq[ks] = qop((c + 1) % NCT, ks);
+            };
+            step_segment<D, NCT>(st, c, pprev, va, ring[(u + 1) % 3], q, s1[c < NCT ? c : 0], x, e,
+                                 next_q);
             if (c > 0) add_row_sums(st.lpart[c - 1], pprev);
             if (c < NCT) {
 #pragma unroll
