@@ -382,6 +382,164 @@ __device__ __forceinline__ int lane_page_id(const PagedSrc& src, int c0, int t_e
   return page;
 }
 
+// ---- Key tiles through one buffer descriptor per pool ----
+//
+// For pools under 4 GiB (the caller checks): one descriptor per pool, with a
+// tile's byte offset as the loads' scalar offset — a step costs two
+// v_readlane instead of a descriptor per tile (about 17 scalar instructions
+// each, which a lone wave per SIMD pays in issue slots).  Rows past key_end
+// are then real pool memory: the streams mask their scores like any key past
+// a column's limit and zero their V rows in registers.
+
+template <int D>
+struct PoolTiles {
+  __amdgpu_buffer_rsrc_t kd, vd;
+  const PagedSrc* src;
+  int t_end, lane, tpp;
+  __device__ __forceinline__ PoolTiles(const PagedSrc& s, int t_end_, int lane_)
+      : kd(coherent_rsrc(s.k_pool, s.pool_bytes)), vd(coherent_rsrc(s.v_pool, s.pool_bytes)), src(&s),
+        t_end(t_end_), lane(lane_), tpp(s.page_size >> 4) {}
+  // Tile c0 + lane of the chunk at c0, or its last tile for lanes past it:
+  // lane ka + 1 then always holds a step's second tile (the last tile again
+  // when it is missing: its keys masked, its V rows zeroed), with no
+  // cross-lane step (the extra page-id loads hit the same lines).
+  __device__ __forceinline__ int lane_tile(int c0) const { return c0 + min(lane, t_end - c0 - 1); }
+  __device__ __forceinline__ int lane_page(int c0) const {
+    int64_t pg = src->bt_row[magic_div(lane_tile(c0), src->tpp_magic)];
+    if (pg < 0 || pg >= src->n_pages) {
+      set_err(src->err, CIE_ERRBIT_PAGE);
+      pg = 0;
+    }
+    return (int)pg;
+  }
+  // byte offset in the pool of that tile (page, head and in-page rows)
+  __device__ __forceinline__ uint32_t lane_offset(int c0, int page) const {
+    const int t = lane_tile(c0);
+    const int in_page = t - magic_div(t, src->tpp_magic) * tpp;
+    return (uint32_t)(((int64_t)page * src->page_stride + src->head_off + (int64_t)(in_page * 16) * D) * 2);
+  }
+};
+
+// The chunk of up to 64 tiles at c0: its lane offsets and step bookkeeping.
+struct PoolChunk {
+  uint32_t toff;
+  int c0, n_chunk, n_pairs;
+  template <int D>
+  __device__ __forceinline__ PoolChunk(const PoolTiles<D>& pool, int c0_, int page)
+      : toff(pool.lane_offset(c0_, page)), c0(c0_), n_chunk(min(kWave, pool.t_end - c0_)),
+        n_pairs((min(kWave, pool.t_end - c0_) + 1) >> 1) {}
+  // The first step that needs masking or V-row zeroing against limit (a key
+  // at or past it, or a missing second tile): the condition only grows with
+  // the step, so each step tests one scalar instead of recomputing its keys.
+  // Step j < n_pairs holds keys [16 * (c0 + 2j), + 32): it qualifies iff
+  // 16 * (c0 + 2j) + 32 > limit, or its second tile is missing
+  // (2j + 1 == n_chunk).
+  __device__ __forceinline__ int first_step_past(int limit) const {
+    const int x = limit - 32 - 16 * c0;  // in int range: keys < 2^31 - 32
+    int j = x < 0 ? 0 : x / 32 + 1;
+    if (n_chunk & 1) j = min(j, n_pairs - 1);
+    return uniform(j);
+  }
+  // byte offsets of step j's two tiles (past the last step: the last step's)
+  __device__ __forceinline__ void offsets(int j, uint32_t& oa, uint32_t& ob) const {
+    const int ka = 2 * min(j, n_pairs - 1);
+    oa = __builtin_amdgcn_readlane(toff, ka);
+    ob = __builtin_amdgcn_readlane(toff, ka + 1);
+  }
+  // first keys of step j's two tiles (kNoKey for a missing second tile)
+  __device__ __forceinline__ void step_keys(int j, int& ka, int& kb) const {
+    const int a = 2 * min(j, n_pairs - 1);
+    ka = (c0 + a) * 16;
+    kb = a + 1 < n_chunk ? ka + 16 : kNoKey;
+  }
+};
+
+// One K load (n < 2 * KS: tile n % 2, k-step n / 2) or V load (n < 8: tile
+// n / 4, row 4 * grp + n % 4) of a step whose tile offsets are o; ko / vo:
+// the lane's offsets inside a tile (TileLaneOffsets).
+template <int D>
+__device__ __forceinline__ void pool_load_k(KVPair<D>& kv, __amdgpu_buffer_rsrc_t kd, const uint32_t (&o)[2],
+                                            uint32_t ko, int n) {
+  const int t = n % 2, ks = n / 2;
+  kv.k[t][ks] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(kd, ko + 64 * ks, o[t], 0));
+}
+template <int D, int VPOL = 0>
+__device__ __forceinline__ void pool_load_v(KVPair<D>& kv, __amdgpu_buffer_rsrc_t vd, const uint32_t (&o)[2],
+                                            uint32_t vo, int n) {
+  typedef typename HVec<Geo<D>::NT>::type vrow_t;
+  const int t = n / 4, e = n % 4;
+  if constexpr (Geo<D>::NT == 4)
+    kv.v[n] = __builtin_bit_cast(vrow_t, __builtin_amdgcn_raw_buffer_load_b64(vd, vo + e * D * 2, o[t], VPOL));
+  else
+    kv.v[n] = __builtin_bit_cast(vrow_t, __builtin_amdgcn_raw_buffer_load_b128(vd, vo + e * D * 2, o[t], VPOL));
+}
+
+// stream_tiles (below) through one descriptor per pool: attend_pair steps of
+// one or more column tiles, PF steps of loads in flight; the mixed kernel's
+// one-column-tile items (decode rows) run it.
+template <int D, int NCT, int PF, class QS, class Prologue, int VPOL = 0>
+__device__ __forceinline__ void stream_tiles_pool(SoftmaxAcc<D, NCT>& st, const QS& qop,
+                                                  const int (&lim)[NCT], int t_begin, int t_end,
+                                                  int key_end, const PagedSrc& src, float scale_log2,
+                                                  int r16, int grp, Prologue prologue) {
+  t_begin = uniform(t_begin);
+  t_end = uniform(t_end);
+  key_end = uniform(key_end);
+  if (t_begin >= t_end) {
+    prologue();
+    return;
+  }
+  int mask_from = kNoKey;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) mask_from = min(mask_from, lim[c]);
+  // (kept in a vector register, as in stream_tiles)
+  for (int off = 1; off < kWave; off <<= 1) mask_from = min(mask_from, __shfl_xor(mask_from, off, kWave));
+  const int lane = threadIdx.x & (kWave - 1);
+  const TileLaneOffsets<D> lanes(r16, grp);
+  const PoolTiles<D> pool(src, t_end, lane);
+  const __amdgpu_buffer_rsrc_t k_none = coherent_rsrc(src.k_pool, 0);
+  const __amdgpu_buffer_rsrc_t v_none = coherent_rsrc(src.v_pool, 0);
+  int page = pool.lane_page(t_begin);
+  prologue();  // while the first page ids are in flight
+  for (int c0 = t_begin; c0 < t_end; c0 += kWave) {
+    if (c0 != t_begin) page = pool.lane_page(c0);
+    const PoolChunk ch(pool, c0, page);
+    const int j_tail = ch.first_step_past(key_end);
+    KVPair<D> ring[PF + 1];
+    int keya[PF + 1], keyb[PF + 1];
+    // every iteration issues one step's loads, so the wait before a step's
+    // math covers that step's loads only; past the last step they go
+    // through descriptors of no records (zeros, no memory access)
+    auto issue = [&](int slot, int j) {
+      uint32_t o[2];
+      ch.offsets(j, o[0], o[1]);
+      uint32_t ko = lanes.k, vo = lanes.v;
+      asm volatile("" : "+v"(ko), "+v"(vo));
+      const bool real = j < ch.n_pairs;
+      const __amdgpu_buffer_rsrc_t kd = real ? pool.kd : k_none;
+      const __amdgpu_buffer_rsrc_t vd = real ? pool.vd : v_none;
+#pragma unroll
+      for (int n = 0; n < 2 * Geo<D>::KS; ++n) pool_load_k<D>(ring[slot], kd, o, ko, n);
+#pragma unroll
+      for (int n = 0; n < 8; ++n) pool_load_v<D, VPOL>(ring[slot], vd, o, vo, n);
+      ch.step_keys(j, keya[slot], keyb[slot]);
+    };
+#pragma unroll
+    for (int j = 0; j < PF; ++j) issue(j, j);
+    for (int j0 = 0; j0 < ch.n_pairs; j0 += PF + 1) {
+#pragma unroll
+      for (int u = 0; u <= PF; ++u) {
+        const int j = j0 + u;
+        issue((u + PF) % (PF + 1), j + PF);
+        if (j < ch.n_pairs) {
+          if (j >= j_tail) zero_tail_rows<D>(ring[u], keya[u], keyb[u], key_end, grp);
+          attend_pair<D, NCT, QS>(st, ring[u], qop, keya[u], keyb[u], lim, mask_from, scale_log2, grp);
+        }
+      }
+    }
+  }
+}
+
 // Stream key tiles [t_begin, t_end) of one wave through attend_pair, two
 // tiles per step.  The page ids of up to 64 tiles are gathered first, one per
 // lane, so a step's K/V loads depend on no other load; a ring of PF + 1
@@ -625,9 +783,9 @@ __device__ __forceinline__ void add_row_sums(float& lpart, const f16x8& p) {
 // slots).  Rows past key_end are then real pool memory: their scores are
 // masked like any key past a column's limit, and their V rows are zeroed in
 // registers on the steps that hold them (pool memory past a sequence's end
-// may hold anything).  Past the last step the loads repeat the last step's
-// tiles (cache hits), so every step issues the same loads and each wait
-// covers exactly the step it is for.
+// may hold anything).  Past the last step the loads go through descriptors
+// of no records (zeros, no memory access), so every step issues the same
+// loads and each wait covers exactly the step it is for.
 template <int D, int NCT, class QS, class Lim, class Prologue>
 __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, const QS& qop,
                                                        const Lim& lim, int t_begin,
@@ -635,7 +793,6 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
                                                        const PagedSrc& src, float scale_log2,
                                                        int r16, int grp, Prologue prologue) {
   constexpr int NT = Geo<D>::NT;
-  typedef typename HVec<NT>::type vrow_t;
   t_begin = uniform(t_begin);
   t_end = uniform(t_end);
   key_end = uniform(key_end);
@@ -649,95 +806,44 @@ __device__ __forceinline__ void stream_tiles_pipelined(SoftmaxAcc<D, NCT>& st, c
   for (int off = 1; off < kWave; off <<= 1) mask_from = min(mask_from, __shfl_xor(mask_from, off, kWave));
   mask_from = uniform(mask_from);
   const int lane = threadIdx.x & (kWave - 1);
-  const int tpp = src.page_size >> 4;
   const TileLaneOffsets<D> lanes(r16, grp);
-  const __amdgpu_buffer_rsrc_t kd = coherent_rsrc(src.k_pool, src.pool_bytes);
-  const __amdgpu_buffer_rsrc_t vd = coherent_rsrc(src.v_pool, src.pool_bytes);
-  // Tile c0 + lane of the chunk at c0, or its last tile for lanes past it:
-  // lane ka + 1 then always holds a step's second tile (the last tile again
-  // when it is missing: its keys masked, its V rows zeroed), with no
-  // cross-lane step (the extra page-id loads hit the same lines).
-  auto lane_tile = [&](int c0) { return c0 + min(lane, t_end - c0 - 1); };
-  auto lane_pages = [&](int c0) {
-    int64_t pg = src.bt_row[magic_div(lane_tile(c0), src.tpp_magic)];
-    if (pg < 0 || pg >= src.n_pages) {
-      set_err(src.err, CIE_ERRBIT_PAGE);
-      pg = 0;
-    }
-    return (int)pg;
-  };
-  // byte offset in the pool of that tile (page, head and in-page rows)
-  auto lane_offsets = [&](int c0, int page) {
-    const int t = lane_tile(c0);
-    const int in_page = t - magic_div(t, src.tpp_magic) * tpp;
-    return (uint32_t)(((int64_t)page * src.page_stride + src.head_off + (int64_t)(in_page * 16) * D) * 2);
-  };
-  int page = lane_pages(t_begin);
+  const PoolTiles<D> pool(src, t_end, lane);
+  const __amdgpu_buffer_rsrc_t k_none = coherent_rsrc(src.k_pool, 0);
+  const __amdgpu_buffer_rsrc_t v_none = coherent_rsrc(src.v_pool, 0);
+  int page = pool.lane_page(t_begin);
   prologue();
   for (int c0 = t_begin; c0 < t_end; c0 += kWave) {
-    const int n_chunk = min(kWave, t_end - c0);
-    if (c0 != t_begin) page = lane_pages(c0);
-    const uint32_t toff = lane_offsets(c0, page);
-    const int n_pairs = (n_chunk + 1) >> 1;
-    // The first steps that need masking (a key at or past some column's
-    // limit, or a missing second tile) and V-row zeroing (a key at or past
-    // key_end): both conditions only grow with the step, so each step tests
-    // one scalar instead of recomputing its keys.  Step j < n_pairs holds
-    // keys [16 * (c0 + 2j), + 32), so it needs masking iff
-    // 16 * (c0 + 2j) + 32 > mask_from (the same with key_end), or its
-    // second tile is missing (2j + 1 == n_chunk).
-    auto first_step_past = [&](int limit) {
-      const int x = limit - 32 - 16 * c0;  // in int range: keys < 2^31 - 32
-      int j = x < 0 ? 0 : x / 32 + 1;
-      if (n_chunk & 1) j = min(j, n_pairs - 1);
-      return uniform(j);
-    };
-    const int j_mask = first_step_past(mask_from);
-    const int j_tail = first_step_past(key_end);
+    if (c0 != t_begin) page = pool.lane_page(c0);
+    const PoolChunk ch(pool, c0, page);
+    const int n_pairs = ch.n_pairs;
+    // the first steps that need masking and V-row zeroing
+    const int j_mask = ch.first_step_past(mask_from);
+    const int j_tail = ch.first_step_past(key_end);
     KVPair<D> ring[3];  // K in slot t % 3, V in slot t % 2
-    // byte offsets of step j's two tiles
-    auto offsets = [&](int j, uint32_t& oa, uint32_t& ob) {
-      const int ka = 2 * min(j, n_pairs - 1);
-      oa = __builtin_amdgcn_readlane(toff, ka);
-      ob = __builtin_amdgcn_readlane(toff, ka + 1);
-    };
     // (the lane offsets pass through an empty asm at each use, so the
     // compiler cannot hoist "offset + constant" out of the loop into extra
     // registers; the constants then go into the loads' immediate offsets)
+    // (past the last step the loads go through descriptors of no records:
+    // zeros, no memory access)
     auto issue_k = [&](int slot, int j) {
       uint32_t o[2];
-      offsets(j, o[0], o[1]);
+      ch.offsets(j, o[0], o[1]);
       uint32_t ko = lanes.k;
       asm volatile("" : "+v"(ko));
+      const __amdgpu_buffer_rsrc_t kd = j < n_pairs ? pool.kd : k_none;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int ks = 0; ks < Geo<D>::KS; ++ks)
-          ring[slot].k[t][ks] =
-              __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(kd, ko + 64 * ks, o[t], 0));
+      for (int n = 0; n < 2 * Geo<D>::KS; ++n) pool_load_k<D>(ring[slot], kd, o, ko, n);
     };
     auto issue_v = [&](int slot, int j) {
       uint32_t o[2];
-      offsets(j, o[0], o[1]);
+      ch.offsets(j, o[0], o[1]);
       uint32_t vo = lanes.v;
       asm volatile("" : "+v"(vo));
+      const __amdgpu_buffer_rsrc_t vd = j < n_pairs ? pool.vd : v_none;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if constexpr (NT == 4)
-            ring[slot].v[4 * t + e] = __builtin_bit_cast(
-                vrow_t, __builtin_amdgcn_raw_buffer_load_b64(vd, vo + e * D * 2, o[t], 0));
-          else
-            ring[slot].v[4 * t + e] = __builtin_bit_cast(
-                vrow_t, __builtin_amdgcn_raw_buffer_load_b128(vd, vo + e * D * 2, o[t], 0));
-        }
+      for (int n = 0; n < 8; ++n) pool_load_v<D>(ring[slot], vd, o, vo, n);
     };
-    auto step_keys = [&](int j, int& ka, int& kb) {
-      const int a = 2 * min(j, n_pairs - 1);
-      ka = (c0 + a) * 16;
-      kb = a + 1 < n_chunk ? ka + 16 : kNoKey;
-    };
+    auto step_keys = [&](int j, int& ka, int& kb) { ch.step_keys(j, ka, kb); };
     issue_k(0, 0);
     issue_v(0, 0);
     issue_k(1, 1);

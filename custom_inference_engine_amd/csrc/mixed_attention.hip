@@ -119,9 +119,10 @@ template <int D>
 constexpr int col_group() {
   return D <= 64 ? CIE_MIXED_CG : 1;
 }
-// The key stream of a work item of several column tiles at D = 64, when the
-// pools are under 4 GiB: stream_tiles_pipelined (steps overlapped, one
-// descriptor per pool); otherwise stream_tiles.
+// The key stream of a work item when the pools are under 4 GiB: of several
+// column tiles at D = 64, stream_tiles_pipelined (steps overlapped, one
+// descriptor per pool); else stream_tiles_pool (one descriptor per pool).
+// Pools of 4 GiB or more: stream_tiles (a descriptor per tile).
 template <int D>
 constexpr bool mixed_pipelined() {
   return D == 64 && CIE_MIXED_PIPELINED;
@@ -228,7 +229,10 @@ __device__ __forceinline__ int seq_cg(const SeqInfo& s) {
 // divisions by constants).
 template <int CG>
 __device__ __forceinline__ int n_col_groups(int n, int cg) {
-  return cg == CG ? (n + CG - 1) / CG : (n + CG / 2 - 1) / (CG / 2);
+  if constexpr (CG < 2)
+    return n;
+  else
+    return cg == CG ? (n + CG - 1) / CG : (n + CG / 2 - 1) / (CG / 2);
 }
 
 // CG = column tiles per group, W = wavefronts per workgroup (template
@@ -419,6 +423,10 @@ __device__ __forceinline__ void run_group(const MixedParams& p, const SeqInfo& s
     if constexpr (P32 && mixed_pipelined<D>() && NCT >= 2)
       stream_tiles_pipelined<D, NCT>(st, QLds<D>{sm_q, lane}, lims, w0, w1, tp.key_end, src,
                                      p.scale_log2, r16, grp, stage_q);
+    else if constexpr (P32)
+      stream_tiles_pool<D, NCT, stream_pf<D, NCT>(), QLds<D>, decltype(stage_q),
+                        NCT == 1 && CIE_MIXED_NARROW_NT ? kBufNt : 0>(
+          st, QLds<D>{sm_q, lane}, lim, w0, w1, tp.key_end, src, p.scale_log2, r16, grp, stage_q);
     else
       stream_tiles<D, NCT, stream_pf<D, NCT>(), QLds<D>, decltype(stage_q),
                    NCT == 1 && CIE_MIXED_NARROW_NT ? kBufNt : 0>(
