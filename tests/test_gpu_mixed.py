@@ -64,6 +64,10 @@ def test_mixed_shapes(native_lib, prior, new):
     ([5000, 3000], [1, 33], 128),
     ([30000], [1], 64),               # one decode row past the chunk cap (16 chunks of its keys)
     ([30000, 9, 700], [1, 1, 1], 128),
+    # past 65,536 keys a wave's share of a chunk spans more than one 64-tile
+    # run of lane offsets (both streams' per-run thresholds and lane tiles)
+    ([70000, 70000, 3], [20, 1, 40], 64),
+    ([70001, 3], [1, 17], 128),
 ], ids=lambda x: str(x))
 def test_mixed_long_prefixes_split_keys(native_lib, prior, new, d):
     case = inputs.make_case(prior, new, seed=37, d=d)
