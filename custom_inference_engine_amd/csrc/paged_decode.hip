@@ -527,16 +527,18 @@ void decode_kernel(DecodeParams p) {
     // Ring of kPF + 1 register-staged pairs: pair j's loads are issued kPF
     // steps before its math, so up to kPF pairs of loads are in flight.
     // Every iteration issues exactly one pair, so the wait before a pair's
-    // math covers that pair's loads only.  Past the end it loads the last
-    // pair again, its V rows from the K pool: those K lines were just read
-    // (cached), while V rows, read non-temporal, would come from HBM again
-    // and hold up the wave's final vmcnt(0) before its arrival atomic.
+    // math covers that pair's loads only.  Past the end the pair it issues
+    // reads cached lines — the new token's row (append mode), or the last
+    // pair's K lines for both K and V — because re-read V rows, loaded
+    // non-temporal, would come from HBM again and hold up the wave's final
+    // vmcnt(0) before its arrival atomic.
     constexpr int kPF = CIE_DECODE_PF;
     KVPair<D> ring[kPF + 1];
     TileLoc loc[kPF + 1][2];
     int keya[kPF + 1], keyb[kPF + 1];
     auto issue = [&](int slot_i, int j) {
-      const f16* vpool = j < n_pairs ? src.v_pool : src.k_pool;
+      const bool real = j < n_pairs;
+      const f16* vpool = real ? src.v_pool : src.k_pool;
       j = min(j, n_pairs - 1);
       const int ka = 2 * j;                // chunk-local index of tile A
       const bool two = ka + 1 < n_chunk;
@@ -550,11 +552,11 @@ void decode_kernel(DecodeParams p) {
                                (int64_t)((tb % tpp) * 16) * D};
       keya[slot_i] = ta * 16;
       keyb[slot_i] = two ? tb * 16 : kNoKey;
-      // (the rope variant re-reads V: it has no registers to spare for the
-      // second address set)
-      if constexpr (kRope)
-        load_pair_new<D, kAppend>(ring[slot_i], src, loc[slot_i][0], loc[slot_i][1], keya[slot_i],
-                                  keyb[slot_i], nr, r16, grp);
+      if constexpr (kAppend)
+        // past the end every lane reads the new token's row (cached), as
+        // the lanes of keys at or past pos do: no second address set
+        load_pair_new<D, kAppend>(ring[slot_i], src, loc[slot_i][0], loc[slot_i][1],
+                                  real ? keya[slot_i] : pos, real ? keyb[slot_i] : pos, nr, r16, grp);
       else
         load_pair_from<D, kAppend>(ring[slot_i], src, vpool, loc[slot_i][0], loc[slot_i][1],
                                    keya[slot_i], keyb[slot_i], nr, r16, grp);
