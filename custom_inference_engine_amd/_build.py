@@ -46,6 +46,11 @@ HIPCC_FLAGS = [
     # always finite): lets max trees use v_max3 without canonicalizing moves
     "-fno-honor-nans",
     "-munsafe-fp-atomics",
+    # kernel-argument preloading: a kernel's first 3 scalar arguments arrive
+    # in SGPRs with the wave (the code object keeps a prologue that loads them
+    # on firmware without preloading).  decode_kernel passes the pointers its
+    # first loads need there, so they do not wait for the argument load.
+    "-mllvm", "-amdgpu-kernarg-preload-count=3",
 ]
 
 
