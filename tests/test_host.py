@@ -122,6 +122,10 @@ def test_default_split_policy():
     assert core.default_decode_splits(16, 2) == 8
     assert core.default_decode_splits(1, 2) == core.DECODE_MAX_SPLITS
     assert core.default_decode_splits(4096, 2) == 1
+    # never past one workgroup per CU: 256 // 56 = 4 (not round(4.57) = 5)
+    assert core.default_decode_splits(28, 2) == 4
+    assert core.default_decode_splits(48, 2) == 2
+    assert core.default_decode_splits(72, 2) == 1
 
 
 def test_module_swap_and_fallback():
