@@ -91,27 +91,6 @@ struct NewRow {
 // holds the new token alone, and its wave would otherwise stream a whole
 // extra tile).  With nr.pos < 0 (no append) every lane reads the pool.
 template <int D>
-__device__ __forceinline__ void load_tile_from(f16x8 (&k)[Geo<D>::KS],
-                                               typename HVec<Geo<D>::NT>::type (&v)[4],
-                                               const PagedSrc& src, const f16* vpool, TileLoc tl,
-                                               int kt0, const NewRow<D>& nr, int r16, int grp) {
-  constexpr int KS = Geo<D>::KS;
-  constexpr int NT = Geo<D>::NT;
-  typedef typename HVec<NT>::type vrow_t;
-  auto past = [&](int row) { return nr.pos >= 0 && kt0 + row >= nr.pos; };
-  const f16* kp = past(r16) ? nr.k + 8 * grp : src.k_pool + tl.base + r16 * D + 8 * grp;
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) k[ks] = *reinterpret_cast<const f16x8*>(kp + 32 * ks);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int row = 4 * grp + e;
-    const f16* vp = past(row) ? nr.v + NT * r16 : vpool + tl.base + row * D + NT * r16;
-    v[e] = stream_load(reinterpret_cast<const vrow_t*>(vp));
-  }
-}
-
-// As load_tile_from, V rows from src.v_pool.
-template <int D>
 __device__ __forceinline__ void load_tile_new(f16x8 (&k)[Geo<D>::KS],
                                               typename HVec<Geo<D>::NT>::type (&v)[4],
                                               const PagedSrc& src, TileLoc tl, int kt0,
@@ -144,24 +123,6 @@ __device__ __forceinline__ void load_pair_new(KVPair<D>& kv, const PagedSrc& src
   } else {
     load_tile_new<D>(kv.k[0], *reinterpret_cast<vquad_t*>(&kv.v[0]), src, t0, key0a, nr, r16, grp);
     load_tile_new<D>(kv.k[1], *reinterpret_cast<vquad_t*>(&kv.v[4]), src, t1, key0b, nr, r16, grp);
-  }
-}
-
-// As load_pair_new, V rows from vpool (src.v_pool, or src.k_pool for a step
-// past the end).
-template <int D, bool kAppend>
-__device__ __forceinline__ void load_pair_from(KVPair<D>& kv, const PagedSrc& src, const f16* vpool,
-                                               TileLoc t0, TileLoc t1, int key0a, int key0b,
-                                               const NewRow<D>& nr, int r16, int grp) {
-  typedef typename HVec<Geo<D>::NT>::type vrow_t;
-  typedef vrow_t vquad_t[4];
-  if constexpr (!kAppend) {
-    load_pair<D>(kv, src.k_pool, vpool, t0, t1, r16, grp);
-  } else {
-    load_tile_from<D>(kv.k[0], *reinterpret_cast<vquad_t*>(&kv.v[0]), src, vpool, t0, key0a, nr, r16,
-                      grp);
-    load_tile_from<D>(kv.k[1], *reinterpret_cast<vquad_t*>(&kv.v[4]), src, vpool, t1, key0b, nr, r16,
-                      grp);
   }
 }
 
@@ -564,8 +525,7 @@ void decode_kernel(const int64_t* __restrict__ a_slot_ids, const int32_t* __rest
         load_pair_new<D, kAppend>(ring[slot_i], src, loc[slot_i][0], loc[slot_i][1],
                                   real ? keya[slot_i] : pos, real ? keyb[slot_i] : pos, nr, r16, grp);
       else
-        load_pair_from<D, kAppend>(ring[slot_i], src, vpool, loc[slot_i][0], loc[slot_i][1],
-                                   keya[slot_i], keyb[slot_i], nr, r16, grp);
+        load_pair<D>(ring[slot_i], src.k_pool, vpool, loc[slot_i][0], loc[slot_i][1], r16, grp);
     };
 #pragma unroll
     for (int j = 0; j < kPF; ++j) issue(j, j);
