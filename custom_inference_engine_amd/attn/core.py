@@ -484,8 +484,10 @@ def mixed_gqa_attention(q, k, v, max_seqlen: int, cu_seqlens, kv_lens, slot_ids,
     prior lengths; row i of sequence b attends keys [0, kv_lens[b] + i].
     Rows outside every sequence are left as ``torch.empty_like`` leaves them.
     ``partials_bytes`` is the budget of split-chunk partial state (default
-    ``cie_mixed_partials_bytes``: 2 rows per token and q head); sequences
-    whose split tiles do not fit it run unsplit, with the same results.
+    ``cie_mixed_partials_bytes``: per q head, the larger of 2 rows per token
+    and 16 rows for each of the first 64 tokens, so the decode rows of a
+    small batch can all split); sequences whose split tiles do not fit it
+    run unsplit, with the same results.
     ``plan``: the step's ``mixed_plan`` (same batch, ``total_T``, heads and
     budget); ``cu_seqlens``, ``kv_lens`` and ``slot_ids`` are then read from it.
     """

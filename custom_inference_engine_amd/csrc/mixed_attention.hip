@@ -1371,8 +1371,15 @@ static int64_t mixed_partial_rows(int64_t bytes, int64_t D) {
   return r < 0 ? 0 : (r > kMaxPartRows ? kMaxPartRows : r);
 }
 
-// The default budget: kDefaultRowsPerToken chunk rows per token and q head.
+// The default budget, per q head: kDefaultRowsPerToken chunk rows per token,
+// and at least kMaxChunks rows for each of the first kDefaultChunkedTokens
+// tokens.  A decode row (one token) whose keys split into up to kMaxChunks
+// chunks needs that many rows; in a batch of mostly decode rows the
+// per-token allowance alone would leave most of them unsplit, each row's
+// keys streamed by one workgroup (32 rows of 16,384 keys + a 16-token
+// prefill: 101.8 us at 2 rows per token, 56.9 at 16).
 constexpr int64_t kDefaultRowsPerToken = 2;
+constexpr int64_t kDefaultChunkedTokens = 64;
 
 }  // namespace cie
 
@@ -1380,7 +1387,9 @@ using namespace cie;
 
 extern "C" int64_t cie_mixed_partials_bytes(int64_t total_T, int64_t H_q, int64_t D) {
   if (total_T < 0 || H_q <= 0 || D <= 0 || total_T > ((int64_t)1 << 40) / H_q) return -1;
-  int64_t rows = kDefaultRowsPerToken * total_T * H_q;
+  const int64_t per_token = kDefaultRowsPerToken * total_T;
+  const int64_t chunked = kMaxChunks * (total_T < kDefaultChunkedTokens ? total_T : kDefaultChunkedTokens);
+  int64_t rows = (per_token > chunked ? per_token : chunked) * H_q;
   if (rows > kMaxPartRows) rows = kMaxPartRows;
   return mixed_layout(rows, D).total;
 }

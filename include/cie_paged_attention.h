@@ -332,9 +332,11 @@ int cie_kv_append_tokens_qkv_rope(void* q_out, void* k_pool, void* v_pool,
  *                the budget, in sequence order, are split; the rest run
  *                unsplit — same results, longer critical path.  A row takes
  *                4 * (D + 2) bytes; the budget caps at 2,097,088 rows.
- *                cie_mixed_partials_bytes(total_T, H_q, D) is the default,
- *                2 rows per token and q head (about 7.8 MB for 1,052 tokens,
- *                14 heads, D = 64); partials may be NULL with
+ *                cie_mixed_partials_bytes(total_T, H_q, D) is the default:
+ *                per q head, the larger of 2 rows per token and 16 rows (a
+ *                decode row's most chunks) for each of the first 64 tokens
+ *                (about 7.8 MB for 1,052 tokens, 14 heads, D = 64; 3.8 MB
+ *                at most below 512 tokens); partials may be NULL with
  *                partials_bytes = 0 (nothing splits).
  *   counters   : cie_mixed_counters(B, H_kv, max_seqlen) int32, 16-byte
  *                aligned, zero before the call and left zero by it (an

@@ -66,6 +66,12 @@ def test_workspace_sizes(native_lib):
     assert native_lib.cie_mixed_partials_bytes(10**6, 64, 128) < 2_097_088 * 130 * 4 + 1024
     assert native_lib.cie_mixed_partials_bytes(0, 14, 64) >= 0
     assert native_lib.cie_mixed_partials_bytes(10, 0, 64) == -1
+    # small batches (mostly decode rows): 16 rows (a row's most chunks) for
+    # each of the first 64 tokens, so every decode row can split
+    row = 66 * 4
+    assert native_lib.cie_mixed_partials_bytes(28, 14, 64) >= 16 * 28 * 14 * row
+    assert native_lib.cie_mixed_partials_bytes(100, 14, 64) >= 16 * 64 * 14 * row
+    assert native_lib.cie_mixed_partials_bytes(100, 14, 64) < 16 * 64 * 14 * row + 1024
     # an arrival word and a stale word per (tile, column group)
     n = native_lib.cie_mixed_counters(32, 2, 256)
     assert n >= 2 * 32 * 2 * 16 and n % 2 == 0

@@ -400,11 +400,33 @@ def _written_m_rows(ws, cap):
     return (~torch.isnan(m)).nonzero().flatten()
 
 
+def test_mixed_partials_decode_rows_default_budget(native_lib):
+    """A batch of mostly long decode rows (12 rows of 6,000-8,200 keys, 7 to
+    11 chunks each, and one 8-token prefill): the default budget's floor of
+    16 rows per token for the first 64 tokens lets every decode row split —
+    the call writes exactly the rows all their chunks need — and the result
+    matches the oracle."""
+    prior = [0] + [6000 + 200 * i for i in range(12)]
+    new = [8] + [1] * 12
+    case = inputs.make_case(prior, new, seed=45)
+    ms = 8
+    need = _split_partial_rows(prior, new, 14, 2, 1)
+    assert all(r > 0 for r in need[1:]) and need[0] == 0
+    nbytes = _native.load().cie_mixed_partials_bytes(case.T, 14, 64)
+    assert 2 * case.T * 14 < sum(need) <= (nbytes - 768) // (4 * 66)
+    note(f"mixed decode rows, default partials budget ({nbytes} bytes, {sum(need)} rows)")
+    o, ws, canary, clean = _mixed_with_budget(case, nbytes, ms)
+    assert canary and clean
+    rows = _written_m_rows(ws, (nbytes - 768) // (4 * 66))
+    assert rows.numel() == sum(need) and int(rows.max()) == sum(need) - 1
+    _check(case, o, "decode rows, default partials budget")
+
+
 def test_mixed_partials_config3_default_budget(native_lib):
     """Config 3 takes 504 partial rows (its decode rows split, its prefill
-    chunks do not), well inside the default budget (2 rows per token and
-    head, under 8 MB): the call writes exactly rows [0, 504) of part_m,
-    nothing past its buffer, and matches the oracle."""
+    chunks do not), well inside the default budget (at 1,052 tokens: 2 rows
+    per token and head, under 8 MB): the call writes exactly rows [0, 504)
+    of part_m, nothing past its buffer, and matches the oracle."""
     case = inputs.config3()
     ms = case.meta["max_seqlen"]
     need = _split_partial_rows(case.kv_lens.tolist(), case.new_lens.tolist(), 14, 2, (ms + 15) // 16)
