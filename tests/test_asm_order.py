@@ -130,3 +130,26 @@ def test_rope_rounds_through_fp32(src, kernel, tmp_path):
     for name, body in kernels.items():
         fused = [l.strip() for l in body if FMA_MIX_F16.match(l)]
         assert not fused, f"{name}: {len(fused)} single-rounding fp16 FMAs, e.g. {fused[0]}"
+
+
+PRELOAD = re.compile(r"^\s*\.amdhsa_user_sgpr_kernarg_preload_length\s+(\d+)")
+
+
+def test_decode_start_arguments_are_preloaded(tmp_path):
+    """decode_kernel takes the pointers its first load is indexed by (slot ids,
+    plan) and the plan's grid size as three scalar arguments ahead of its
+    parameter struct, and the library is built to preload three kernel
+    arguments into SGPRs: every decode kernel's descriptor must preload their
+    5 dwords, or the start's first load waits on a kernel-argument load again."""
+    asm = _assembly("paged_decode.hip", tmp_path)
+    lengths, name = {}, None
+    for line in asm.splitlines():
+        m = re.match(r"^\s*\.amdhsa_kernel\s+(\S+)", line)
+        if m:
+            name = m.group(1)
+        m = PRELOAD.match(line)
+        if m and name is not None:
+            lengths[name] = int(m.group(1))
+    decode = {n: v for n, v in lengths.items() if "decode_kernel" in n}
+    assert decode, "no decode_kernel descriptor in the assembly"
+    assert all(v == 5 for v in decode.values()), decode
