@@ -81,8 +81,10 @@ def parse():
                          "--out DIR); the package itself only ever loads the in-tree library")
     ap.add_argument("--trace-out", default=None, metavar="PATH",
                     help="with --trace-mixed: also write every item's stamps to PATH as JSON")
-    ap.add_argument("--mixed-part", choices=("all", "prefill", "decode"), default="all",
-                    help="config 3: time only its prefill chunks or only its decode rows")
+    ap.add_argument("--mixed-part", choices=("all", "prefill", "decode", "long-prefill"), default="all",
+                    help="config 3: time only its prefill chunks or only its decode rows; long-prefill: "
+                         "4 sequences x 2,048 new tokens on no prior (a compute-heavy prefill, for the "
+                         "MFMA counters of large tiles; no reference counterpart)")
     ap.add_argument("--step-modules", action="store_true",
                     help="config 5's model: one mixed step (8 sequences x 64 new tokens over 512 cached, "
                          "token bucket 512) through the eager, full-graph and piecewise step modules")
@@ -778,7 +780,11 @@ def bench_mixed(args, cie, inputs, ref, dev):
     its 28 decode rows alone (the same draws), e.g. to read the MFMA counters
     of the prefill tiles without the decode rows."""
     case = inputs.config3(seed=0)
-    if args.mixed_part != "all":
+    max_seqlen = case.meta["max_seqlen"]
+    if args.mixed_part == "long-prefill":
+        case = inputs.make_case([0] * 4, [2048] * 4, seed=0)
+        max_seqlen = 2048
+    elif args.mixed_part != "all":
         prior, new = case.kv_lens.tolist(), case.new_lens.tolist()
         keep = [i for i, n in enumerate(new) if (n > 1) == (args.mixed_part == "prefill")]
         case = inputs.make_case([prior[i] for i in keep], [new[i] for i in keep], seed=0)
@@ -793,8 +799,8 @@ def bench_mixed(args, cie, inputs, ref, dev):
 
         def f():
             cie.kv_append_tokens(L.kp, L.vp, L.k_new, L.v_new, c.pages, c.offsets)
-            outs[i] = cie.mixed_gqa_attention(L.q, L.kp, L.vp, 256, c.cu_seqlens, c.kv_lens, c.slot_ids,
-                                              c.block_table)
+            outs[i] = cie.mixed_gqa_attention(L.q, L.kp, L.vp, max_seqlen, c.cu_seqlens, c.kv_lens,
+                                              c.slot_ids, c.block_table)
         return f
 
     call(0)()
@@ -809,8 +815,8 @@ def bench_mixed(args, cie, inputs, ref, dev):
     # the mixed kernel alone (the roofline's kernel), on the same rotating layers
     def mixed_only(i):
         L = layers[i]
-        return lambda: cie.mixed_gqa_attention(L.q, L.kp, L.vp, 256, c.cu_seqlens, c.kv_lens, c.slot_ids,
-                                               c.block_table)
+        return lambda: cie.mixed_gqa_attention(L.q, L.kp, L.vp, max_seqlen, c.cu_seqlens, c.kv_lens,
+                                               c.slot_ids, c.block_table)
 
     us_mix, _ = time_calls([mixed_only(i) for i in range(R)], args.steps, args.warmup, not args.no_graph,
                            args.repeats)
@@ -818,7 +824,7 @@ def bench_mixed(args, cie, inputs, ref, dev):
     # Planned launches: a mixed step makes one plan (mixed_plan) for all of
     # its layers, so the timed sequence launches the plan once per
     # PLAN_LAYERS calls, inside the timed region.
-    us_mix_planned, err_planned = time_mixed_planned(cie, layers, c, case, 256, 14, args)
+    us_mix_planned, err_planned = time_mixed_planned(cie, layers, c, case, max_seqlen, 14, args)
     log(f"planned: mixed kernel {us_mix_planned:.2f} us/launch (1 plan per {PLAN_LAYERS} launches), "
         f"planned == unplanned: {err_planned}")
     E = (case.kv_lens + case.new_lens).tolist()
@@ -832,6 +838,8 @@ def bench_mixed(args, cie, inputs, ref, dev):
         flops += 4 * 14 * 64 * keys
     print(json.dumps({
         "metric": "mixed varlen chunked prefill + decode us/call (config 3)" if args.mixed_part == "all"
+        else "mixed varlen attention us/call (4 x 2,048-token prefill, no prior)"
+        if args.mixed_part == "long-prefill"
         else f"mixed varlen attention us/call (config 3, its {args.mixed_part} part only)",
         "value": round(us, 3), "unit": "us/call", "higher_is_better": False, "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6),
@@ -842,7 +850,9 @@ def bench_mixed(args, cie, inputs, ref, dev):
         "dtype": "fp16 (fp32 accumulate)", "data": "synthetic",
         "config": {"workload": {"all": "config 3 mixed: 4x256-row prefill chunks + 28 decode rows",
                                 "prefill": "config 3's 4x256-row prefill chunks alone",
-                                "decode": "config 3's 28 decode rows alone"}[args.mixed_part], "T": case.T,
+                                "decode": "config 3's 28 decode rows alone",
+                                "long-prefill": "4 sequences x 2,048 new tokens on no prior (no reference "
+                                                "counterpart)"}[args.mixed_part], "T": case.T,
                    "algorithmic_bytes": nbytes, "flops": flops, "layer_rotation": R},
         "roofline": {"bound": "mfma", "kernel": "mixed_attention_kernel<64>",
                      "achieved": round(flops / (us_mix * 1e-6) / 1e12, 2), "peak": MFMA_F16_PEAK_TFLOPS,
