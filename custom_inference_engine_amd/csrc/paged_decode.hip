@@ -556,15 +556,28 @@ void decode_kernel(const int64_t* __restrict__ a_slot_ids, const int32_t* __rest
       }
     }
   }
-  if (odd) {
-    if (n_main == 0) {
-      rotate();
-      attend_odd();
-    }
+  // Append mode: if the new token sits in this wave's odd tile, its rows go
+  // to the pool only after the workgroup's arrival (store_odd below): issued
+  // here, their completion would join the wait for the partial stores that
+  // the arrival atomic follows (0.1 us per call at config 2).  Rope mode
+  // stores them here (deferred, its build ran 0.2 us slower).
+  auto store_odd = [&]() {
     if constexpr (kAppend) {
+      if (odd && pos >= xkey && pos < xkey + 16)
+        store_new_row<D>(xt, src, xloc, xloc, xkey, kNoKey, pos, r16, grp);
+    }
+  };
+  if constexpr (kRope) {
+    if (odd) {
+      if (n_main == 0) {
+        rotate();
+        attend_odd();
+      }
       if (pos >= xkey && pos < xkey + 16)
         store_new_row<D>(xt, src, xloc, xloc, xkey, kNoKey, pos, r16, grp);
     }
+  } else if (odd && n_main == 0) {
+    attend_odd();
   }
 
   DECODE_TRACE(2, __builtin_amdgcn_s_memrealtime());
@@ -622,6 +635,7 @@ void decode_kernel(const int64_t* __restrict__ a_slot_ids, const int32_t* __rest
   }
   DECODE_TRACE(9, __builtin_amdgcn_s_memrealtime());
   if (S == 1) {
+    if constexpr (!kRope) store_odd();
     DECODE_TRACE_DUMP();
     return;
   }
@@ -630,6 +644,7 @@ void decode_kernel(const int64_t* __restrict__ a_slot_ids, const int32_t* __rest
   int32_t* const arrival = p.counters + b * p.H_kv + g;
   const bool last = arrive_last(arrival, (int64_t)p.B * p.H_kv, S, &sm_last, p.err);
   DECODE_TRACE(10, __builtin_amdgcn_s_memrealtime());
+  if constexpr (!kRope) store_odd();
   if (!last) {
     DECODE_TRACE_DUMP();
     return;
