@@ -39,7 +39,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 # HBM bytes per launch of the measured kernel, from rocprofv3 FETCH_SIZE x 2.0 +
 # WRITE_SIZE (scale factors from a plain 256 MiB copy), committed under profiles/
 TRAFFIC_BYTES = {
-    2: (70_897_664, "profiles/hbm_traffic_decode_config2.md"),
+    2: (70_906_880, "profiles/hbm_traffic_decode_config2.md"),
     3: (39_666_586, "profiles/mixed_attention_config3.md"),
 }
 HBM_PEAK_GBPS = 8000.0
